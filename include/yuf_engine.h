@@ -1,0 +1,233 @@
+/*
+ * yuf_engine.h -- C ABI of libyufhip.so, the MI355X (gfx950) backend for the
+ * YufMusicGen recurrent hot path.
+ *
+ * The entry points mirror the reference's engine and operator surfaces:
+ *   - the Rust/Vulkan engine API of YufeiV/YufMusicGen (`vulkan/`): checkpoint
+ *     load, model creation, per-token step, state reset, sampling;
+ *   - the Python operators `rwkv7_cuda` and `rosa_householder_scan`
+ *     (`yufmusicgen/cuda_ops.py`, `yufmusicgen/rosa_cuda.py`).
+ * Each declaration cites the reference interface it replaces (file:line).
+ *
+ * Conventions
+ *   - Every int-returning call returns YUF_OK (0) or a negative yuf_status;
+ *     yuf_last_error() then describes the failure (thread-local string).
+ *     Nothing throws or aborts across the ABI.
+ *   - "stream" arguments are hipStream_t passed as void* (NULL = the null
+ *     stream).  Kernel-level calls are asynchronous on that stream.
+ *   - Pointers documented as "device" must point to device memory; "host"
+ *     buffers are caller-owned and only read/written during the call.
+ *   - An engine is single-owner: calls on one engine must not overlap
+ *     (like the reference `Model`, `vulkan/src/compute/model.rs:13-21`).
+ */
+#ifndef YUF_ENGINE_H
+#define YUF_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    YUF_OK = 0,
+    YUF_ERR_INVALID = -1,     /* bad argument / shape / unsupported size */
+    YUF_ERR_IO = -2,          /* file could not be opened or read */
+    YUF_ERR_FORMAT = -3,      /* malformed .yuf (magic, version, header, size) */
+    YUF_ERR_HIP = -4,         /* a HIP runtime call failed */
+    YUF_ERR_OOM = -5,         /* device or host allocation failed */
+    YUF_ERR_RANGE = -6        /* index out of range (token id, stream slot) */
+} yuf_status;
+
+/* Last error message of the calling thread ("" if none). */
+const char *yuf_last_error(void);
+/* Library version string. */
+const char *yuf_version(void);
+
+/* ---------------------------------------------------------------------------
+ * Kernel-level operators (device pointers, asynchronous on `stream`).
+ * ------------------------------------------------------------------------- */
+
+/*
+ * WKV-7 forward scan over B x H independent N x N fp32 states.
+ * Replaces `rwkv7_cuda(r, w, k, v, a, b)` (yufmusicgen/cuda_ops.py:256-266,
+ * op `yufmusicgen_rwkv7::forward`, yufmusicgen/cuda/rwkv7_clampw.cpp:18-33)
+ * and extends it with a non-zero initial state (the stateful path of
+ * yufmusicgen/model.py:145-165).
+ *   r, w_raw, k, v, a, b : device [B, T, H, N] fp32, contiguous.
+ *   state_in             : device [B, H, N, N] (row i = value, col j = key) or
+ *                          NULL for a zero initial state.
+ *   state_out            : device [B, H, N, N] final state or NULL; may alias
+ *                          state_in.
+ *   y                    : device [B, T, H, N] output.
+ * Per step: d = exp(-exp(-0.5) * sigmoid(w_raw)); sa = S a;
+ *           S = S diag(d) + sa b^T + v k^T; y = S r.
+ * Supported N: 8, 16, 32, 40, 48, 64, 128.  T >= 0 (any length, no padding).
+ */
+int yuf_wkv7_scan_f32(int B, int T, int H, int N,
+                      const float *r, const float *w_raw, const float *k,
+                      const float *v, const float *a, const float *b,
+                      const float *state_in, float *state_out, float *y,
+                      void *stream);
+
+/*
+ * ROSA Householder memory scan.
+ * Replaces `rosa_householder_scan(cand, write, read_raw, decay, direction,
+ * memory)` (yufmusicgen/rosa_cuda.py:157-180, op `yufmusicgen_rosa::forward`,
+ * yufmusicgen/cuda/rosa_householder.cpp:24-50).
+ *   cand, write          : device [B, T, D] pre-activations.
+ *   read_raw             : device [B, T, D] read-gate pre-activation, or NULL.
+ *   decay                : device [D], post-sigmoid lambda.
+ *   direction            : device [D], unit Householder vector u.
+ *   memory_in            : device [B, D] or NULL (zero).
+ *   memory_out           : device [B, D] or NULL; may alias memory_in.
+ *   read_out             : device [B, T, D].
+ * m_t = lambda * H(m_{t-1}) + sigmoid(write_t) * tanh(cand_t), H(x) = x - 2(x.u)u;
+ * read_t = H(m_t), times sigmoid(read_raw_t) when read_raw is not NULL
+ * (the gated read of yufmusicgen/model.py:281-287).
+ * Supported D: 1 .. 1024.
+ */
+int yuf_rosa_scan_f32(int B, int T, int D,
+                      const float *cand, const float *write, const float *read_raw,
+                      const float *decay, const float *direction,
+                      const float *memory_in, float *memory_out, float *read_out,
+                      void *stream);
+
+/*
+ * Linear layer on the matrix cores: C = act(A W^T + bias) + residual, fp32.
+ * The projection primitive of every nn.Linear on the path
+ * (yufmusicgen/model.py:107-112, :196, :306-342, :377, :421).
+ *   A [M, K], W [N, K] (nn.Linear weight layout), C [M, N], all row-major,
+ *   device pointers; bias [N] or NULL; residual [M, N] or NULL (may alias C);
+ *   act: 0 none, 1 tanh, 2 sigmoid.
+ */
+int yuf_linear_f32(int M, int N, int K, const float *A, const float *W, const float *bias, int act,
+                   const float *residual, float *C, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Checkpoints (.yuf).  Replaces `Checkpoint::load / tensor / tensor_dims`
+ * (vulkan/src/checkpoint.rs:90-176).
+ * ------------------------------------------------------------------------- */
+
+typedef struct yuf_ckpt yuf_ckpt;
+
+typedef struct {
+    int32_t vocab_size;
+    int32_t d_model;
+    int32_t n_layers;
+    int32_t n_heads;
+    int32_t head_size;
+    int32_t rosa_size;
+    int32_t low_rank;       /* from the w1 tensor's shape, not a formula */
+    int32_t tie_embeddings; /* 0 / 1 */
+    float dropout;
+    int32_t midi_offset;    /* header "midi.midi_offset" (260) */
+    int32_t midi_vocab_size;
+} yuf_model_config;
+
+/* Load and validate a .yuf file (magic "YUFM", version 1, JSON header,
+ * f32 payload whose size must match; checkpoint.rs:90-149). */
+int yuf_ckpt_load(const char *path, yuf_ckpt **out);
+void yuf_ckpt_free(yuf_ckpt *ckpt);
+int yuf_ckpt_config(const yuf_ckpt *ckpt, yuf_model_config *out);
+/* Borrow a tensor by name (checkpoint.rs:151-176): host pointer valid until
+ * yuf_ckpt_free; dims receives up to 8 sizes. */
+int yuf_ckpt_tensor(const yuf_ckpt *ckpt, const char *name, const float **data,
+                    int64_t *count, int32_t *ndim, int64_t dims[8]);
+
+/* ---------------------------------------------------------------------------
+ * Engine: device-resident weights and per-stream recurrent state.
+ * Replaces `Model::new / step / reset_state` (vulkan/src/compute/model.rs:24-65),
+ * batched over many streams and with a real prefill.
+ * ------------------------------------------------------------------------- */
+
+typedef struct yuf_engine yuf_engine;
+
+enum { YUF_LOGITS_NONE = 0, YUF_LOGITS_LAST = 1, YUF_LOGITS_ALL = 2 };
+
+/* Copy the checkpoint's weights to the device (the checkpoint may be freed
+ * afterwards, like model.rs:24-51).  max_streams = state slots kept in HBM;
+ * max_tokens = largest n * T processed per internal pass (longer prefills
+ * are split into T-chunks that carry the state). */
+int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_tokens, yuf_engine **out);
+void yuf_engine_destroy(yuf_engine *eng);
+int yuf_engine_config(const yuf_engine *eng, yuf_model_config *out);
+/* The HIP stream the engine runs its work on (hipStream_t as void*). */
+void *yuf_engine_stream(yuf_engine *eng);
+
+/* Batched prefill of n streams (slots[i] in [0, max_streams)), each by T
+ * tokens, continuing from each stream's current state (the full-sequence
+ * forward of yufmusicgen/model.py:406-422, replacing the reference engine's
+ * per-token prefill loop, vulkan/src/generation.rs:176-185).
+ *   slots  : host [n] int32
+ *   tokens : host [n * T] int32 (row-major [n, T])
+ *   logits : host output, [n, V] for LAST, [n, T, V] for ALL, ignored for NONE.
+ * Synchronous. */
+int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T,
+                const int32_t *tokens, float *logits, int logits_mode);
+
+/* Same with device-resident tokens and logits, asynchronous on the engine's
+ * stream (slots stay host).  Use for throughput measurements. */
+int yuf_prefill_device(yuf_engine *eng, int n, const int32_t *slots, int T,
+                       const int32_t *tokens_dev, float *logits_dev, int logits_mode);
+
+/* One token for each of n streams; logits [n, V] (model.py:424-431;
+ * Model::step, model.rs:54-60).  Host buffers, synchronous. */
+int yuf_step(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens, float *logits);
+
+/* Same with device tokens / logits, asynchronous on the engine's stream. */
+int yuf_step_device(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens_dev,
+                    float *logits_dev);
+
+/* Zero all recurrent state of one slot (slot = -1: every slot), including
+ * the token-shift `previous` vector the reference reset leaves stale
+ * (Model::reset_state, model.rs:62-65). */
+int yuf_state_reset(yuf_engine *eng, int slot);
+/* Bytes of one stream's state blob: per layer [prev d | wkv H*N*N (i,j) | rosa D]
+ * fp32, the order of BlockState (yufmusicgen/model.py:29-38). */
+size_t yuf_state_size(const yuf_engine *eng);
+int yuf_state_save(yuf_engine *eng, int slot, void *host_buf);
+int yuf_state_load(yuf_engine *eng, int slot, const void *host_buf);
+
+/* ---------------------------------------------------------------------------
+ * Sampling.  Replaces `Mt19937` and `sample_token` / `argmax`
+ * (vulkan/src/sampler.rs:22-82, :131-271) and Python `sample_token`
+ * (yufmusicgen/cli/generate.py:45-56).
+ * ------------------------------------------------------------------------- */
+
+/* MT19937 state, caller-owned (the generator of torch.manual_seed). */
+typedef struct {
+    uint32_t mt[624];
+    uint32_t index;
+} yuf_rng;
+
+void yuf_rng_seed(yuf_rng *rng, uint64_t seed);
+uint32_t yuf_rng_next_u32(yuf_rng *rng);
+/* 53-bit uniform in [0,1) from two words (hi << 32 | lo). */
+double yuf_rng_next_uniform(yuf_rng *rng);
+
+/* Host sampling over V logits, token-for-token what torch's CPU
+ * `sample_token` draws under the same seed: temperature <= 0 -> argmax
+ * (first maximum); otherwise scale, optional top_k (> 0: keep the k largest),
+ * sort descending, softmax, drop where cumulative - p > top_p, renormalise,
+ * and torch.multinomial's single-sample path argmax(p / q), q ~ Exp(1).
+ * Returns the token id, or a negative yuf_status. */
+int32_t yuf_sample(const float *logits, int V, float temperature, float top_p, int top_k,
+                   yuf_rng *rng);
+/* First index of the maximum (torch.argmax semantics). */
+int32_t yuf_argmax(const float *logits, int V);
+
+/* Device sampling for n streams at once (no logits copy to the host):
+ * temperature <= 0 -> argmax; otherwise top_k in [1, 64] largest scaled
+ * logits, softmax over them and a Gumbel-max draw from a counter-based
+ * generator keyed by (seed, counter, stream index).  Not bit-compatible with
+ * torch (use yuf_sample for that).  logits_dev [n, V]; tokens_dev [n] int32. */
+int yuf_sample_device(int n, int V, const float *logits_dev, float temperature, int top_k,
+                      uint64_t seed, uint64_t counter, int32_t *tokens_dev, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YUF_ENGINE_H */

@@ -1,0 +1,34 @@
+"""The C-ABI library loads (no GPU needed) and exports every declared entry point."""
+
+import re
+from pathlib import Path
+
+from yufmusicgen_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "yuf_engine.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(yuf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declarations_are_bound():
+    declared = declared_functions()
+    assert len(declared) >= 25
+    assert sorted(_lib.SIGNATURES) == declared
+
+
+def test_library_exports_every_declared_symbol():
+    assert _lib.missing_symbols() == []
+    assert _lib.lib().yuf_version().decode().startswith("yufhip")
+
+
+def test_errors_cross_the_abi_as_status_codes():
+    lib = _lib.lib()
+    # Unsupported head size: rejected before any GPU work.
+    rc = lib.yuf_wkv7_scan_f32(1, 1, 1, 12, *([None] * 10))
+    assert rc == -1 and "head size" in lib.yuf_last_error().decode()
+    rc = lib.yuf_rosa_scan_f32(1, 1, 2048, *([None] * 9))
+    assert rc == -1 and "D must be" in lib.yuf_last_error().decode()

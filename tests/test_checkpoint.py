@@ -1,0 +1,113 @@
+"""The .yuf container: Python writer/reader and the C++ loader behind the ABI.
+
+Checks follow vulkan/src/checkpoint.rs:90-149 (magic, version, JSON header,
+exact payload size) and export_checkpoint.py:32-146 (layout, tensor order).
+"""
+
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+
+from yufmusicgen_amd._lib import YufError
+from yufmusicgen_amd.checkpoint import read_yuf, write_yuf
+from yufmusicgen_amd.config import PRESETS
+from yufmusicgen_amd.engine import Checkpoint
+from yufmusicgen_amd.synth import synth_weights, tensor_specs
+
+
+@pytest.fixture(scope="module")
+def tiny_yuf(tmp_path_factory):
+    cfg = PRESETS["state_test"]
+    path = tmp_path_factory.mktemp("ck") / "tiny.yuf"
+    weights = synth_weights(cfg, seed=3)
+    write_yuf(path, cfg, weights)
+    return path, cfg, weights
+
+
+def test_python_roundtrip_and_export_order(tiny_yuf):
+    path, cfg, weights = tiny_yuf
+    header, tensors = read_yuf(path)
+    assert header["format"] == "yufmusicgen-checkpoint" and header["version"] == 1
+    assert [t["name"] for t in header["tensors"]] == [n for n, _ in tensor_specs(cfg)]
+    # Offsets are contiguous float indices (export_checkpoint.py:90-100).
+    offsets = [t["offset"] for t in header["tensors"]]
+    counts = [t["count"] for t in header["tensors"]]
+    assert offsets == list(np.cumsum([0] + counts[:-1]))
+    # mix_r..mix_g contiguous and in registration order (model.rs:962).
+    names = [t["name"] for t in header["tensors"]]
+    i = names.index("blocks.0.time_mix.mix_r")
+    assert names[i:i + 6] == [f"blocks.0.time_mix.mix_{c}" for c in "rwkvag"]
+    for name, value in weights.items():
+        np.testing.assert_array_equal(tensors[name], value)
+
+
+def test_cpp_loader_matches(tiny_yuf):
+    path, cfg, weights = tiny_yuf
+    ck = Checkpoint.load(path)
+    c = ck.config
+    assert (c["vocab_size"], c["d_model"], c["n_layers"], c["n_heads"], c["head_size"], c["rosa_size"]) == (
+        cfg.vocab_size, cfg.d_model, cfg.n_layers, cfg.n_heads, cfg.head_size, cfg.rosa_size)
+    assert c["low_rank"] == weights["blocks.0.time_mix.w1"].shape[1]
+    assert c["midi_offset"] == 260 and c["tie_embeddings"] == 1
+    for name in ("token_embedding.weight", "blocks.1.time_mix.w2", "blocks.0.rosa.householder", "final_norm.bias"):
+        np.testing.assert_array_equal(ck.tensor(name), weights[name])
+    with pytest.raises(YufError) as err:
+        ck.tensor("no.such.tensor")
+    assert err.value.status == -6
+
+
+def test_low_rank_comes_from_w1_shape(tmp_path):
+    """d_model 1024: Python rounding gives 64, the Rust formula 96 (checkpoint.rs:27-30)."""
+    cfg = PRESETS["wide"]
+    small = type(cfg)(vocab_size=1024, d_model=1024, n_layers=1, n_heads=16, head_size=64, rosa_size=8)
+    assert small.low_rank == 64
+    path = tmp_path / "wide.yuf"
+    write_yuf(path, small, synth_weights(small, seed=0))
+    assert Checkpoint.load(path).config["low_rank"] == 64
+
+
+def _corrupt(path, tmp_path, mutate):
+    data = bytearray(path.read_bytes())
+    out = tmp_path / "bad.yuf"
+    out.write_bytes(bytes(mutate(data)))
+    return out
+
+
+@pytest.mark.parametrize("case", ["magic", "version", "truncated", "extra", "json", "format", "shape"])
+def test_cpp_loader_rejects_malformed_files(tiny_yuf, tmp_path, case):
+    path = tiny_yuf[0]
+    header_len = struct.unpack("<Q", path.read_bytes()[8:16])[0]
+
+    def rewrite_header(data, fn):
+        header = json.loads(bytes(data[16:16 + header_len]))
+        fn(header)
+        blob = json.dumps(header).encode()
+        return data[:8] + struct.pack("<Q", len(blob)) + blob + data[16 + header_len:]
+
+    mutate = {
+        "magic": lambda d: b"NOPE" + d[4:],
+        "version": lambda d: d[:4] + struct.pack("<I", 2) + d[8:],
+        "truncated": lambda d: d[:-4],
+        "extra": lambda d: d + b"\0\0\0\0",
+        "json": lambda d: d[:16] + b"{" * 3 + d[19:],
+        "format": lambda d: rewrite_header(d, lambda h: h.update(format="other")),
+        "shape": lambda d: rewrite_header(d, lambda h: h["tensors"][0].update(shape=[1, 2])),
+    }[case]
+    bad = _corrupt(path, tmp_path, mutate)
+    with pytest.raises(YufError) as err:
+        Checkpoint.load(bad)
+    assert err.value.status == -3, str(err.value)
+
+
+def test_missing_file_is_io_error(tmp_path):
+    with pytest.raises(YufError) as err:
+        Checkpoint.load(tmp_path / "absent.yuf")
+    assert err.value.status == -2
+
+
+def test_golden_fixture_loads(golden_dir):
+    ck = Checkpoint.load(os.path.join(golden_dir, "model_state_test.yuf"))
+    assert ck.config["d_model"] == 32 and ck.config["n_layers"] == 2

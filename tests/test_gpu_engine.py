@@ -1,0 +1,169 @@
+"""GPU parity of the whole engine (prefill, decode, state) against the reference
+golden vectors and the float64 CPU oracle.
+
+Tolerances: logits within 1e-3 absolute; greedy ids
+identical wherever the top-2 logit gap exceeds 1e-3; states within
+1e-4 relative / 1e-5 absolute.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.model import OracleModel, blob_to_state, state_to_blob
+from yufmusicgen_amd.checkpoint import write_yuf
+from yufmusicgen_amd.config import PRESETS
+from yufmusicgen_amd.engine import Checkpoint, Engine, sample_device
+from yufmusicgen_amd.synth import prompt_tokens, synth_weights, uniform_tokens
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_ATOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def state_test(golden_dir):
+    path = os.path.join(golden_dir, "model_state_test.yuf")
+    ck = Checkpoint.load(path)
+    return ck, np.load(os.path.join(golden_dir, "model_state_test.npz"))
+
+
+def _states_from_blob(engine, slots):
+    return np.stack([engine.save_state(s) for s in slots])
+
+
+def test_prefill_matches_reference_golden(state_test):
+    ck, z = state_test
+    eng = Engine(ck, max_streams=4, max_tokens=64)
+    logits = eng.prefill(z["tokens"], logits="all")
+    np.testing.assert_allclose(logits, z["logits"], rtol=0, atol=LOGIT_ATOL)
+    np.testing.assert_allclose(logits, z["logits"], rtol=1e-4, atol=2e-5)
+    blob = _states_from_blob(eng, [0, 1])
+    ref = {k[len("full."):]: v for k, v in z.items() if k.startswith("full.")}
+    cfg = ck.config
+    st = blob_to_state(blob, cfg)
+    for layer, s in enumerate(st):
+        np.testing.assert_allclose(s.previous.numpy(), ref[f"state.{layer}.previous"], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(s.memory.numpy(), ref[f"state.{layer}.memory"], rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(s.rosa.numpy(), ref[f"state.{layer}.rosa"], rtol=1e-4, atol=1e-5)
+
+
+def test_continuation_from_carried_state_matches_reference(state_test):
+    ck, z = state_test
+    eng = Engine(ck, max_streams=2, max_tokens=64)
+    head = eng.prefill(z["tokens"][:, :5], logits="all")
+    tail = eng.prefill(z["tokens"][:, 5:], logits="all")
+    np.testing.assert_allclose(head, z["head_logits"], rtol=1e-4, atol=2e-5)
+    np.testing.assert_allclose(tail, z["tail_logits"], rtol=1e-4, atol=2e-5)
+
+
+def test_step_loop_equals_prefill(state_test):
+    """tests/test_model_state.py:9-28 of the reference, on the engine."""
+    ck, z = state_test
+    tokens = z["tokens"]
+    eng = Engine(ck, max_streams=2, max_tokens=64)
+    full = eng.prefill(tokens, logits="all")
+    eng.reset_state()
+    steps = np.stack([eng.step(tokens[:, t]) for t in range(tokens.shape[1])], axis=1)
+    np.testing.assert_allclose(steps, full, rtol=1e-5, atol=1e-5)
+
+
+def test_state_save_load_reset_and_slots(state_test):
+    ck, z = state_test
+    tokens = z["tokens"]
+    eng = Engine(ck, max_streams=6, max_tokens=64)
+    eng.prefill(tokens[:, :4], slots=[4, 1])
+    saved = eng.save_state(4)
+    ref_tail = eng.prefill(tokens[:1, 4:], slots=[4], logits="all")
+    # Restore into another slot and continue: identical result.
+    eng.load_state(2, saved)
+    again = eng.prefill(tokens[:1, 4:], slots=[2], logits="all")
+    np.testing.assert_array_equal(again, ref_tail)
+    # Reset clears everything, including the token-shift `previous` vector.
+    eng.reset_state(2)
+    assert not np.any(eng.save_state(2))
+    fresh = Engine(ck, max_streams=1, max_tokens=64)
+    np.testing.assert_array_equal(eng.prefill(tokens[:1], slots=[2], logits="all"),
+                                  fresh.prefill(tokens[:1], logits="all"))
+    # Bad slots are errors, not crashes.
+    from yufmusicgen_amd._lib import YufError
+    with pytest.raises(YufError):
+        eng.prefill(tokens[:1], slots=[6])
+    with pytest.raises(YufError):
+        eng.prefill(tokens[:2], slots=[1, 1])
+    with pytest.raises(YufError):
+        eng.step([ck.config["vocab_size"]], slots=[0])
+
+
+def test_chunked_prefill_equals_one_pass(state_test):
+    """max_tokens smaller than n*T forces T-chunks that carry the state."""
+    ck, z = state_test
+    tokens = np.concatenate([z["tokens"]] * 4, axis=1)  # [2, 36]
+    big = Engine(ck, max_streams=2, max_tokens=128).prefill(tokens, logits="all")
+    small = Engine(ck, max_streams=2, max_tokens=10).prefill(tokens, logits="all")
+    np.testing.assert_allclose(small, big, rtol=1e-5, atol=1e-5)
+    last = Engine(ck, max_streams=2, max_tokens=10).prefill(tokens, logits="last")
+    np.testing.assert_allclose(last, big[:, -1], rtol=1e-5, atol=1e-5)
+
+
+def test_tiny_model_prompt_and_greedy_match_reference(golden_dir, tmp_path):
+    z = np.load(os.path.join(golden_dir, "model_tiny.npz"))
+    cfg = PRESETS["tiny"]
+    path = tmp_path / "tiny.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=int(z["seed"]), std=float(z["std"])))
+    eng = Engine(Checkpoint.load(path), max_streams=1, max_tokens=64)
+    logits = eng.prefill(z["prompt"], logits="all")
+    np.testing.assert_allclose(logits, z["prompt_logits"], rtol=0, atol=LOGIT_ATOL)
+    last = logits[0, -1]
+    for i, expect in enumerate(z["greedy"]):
+        top2 = np.sort(last)[-2:]
+        if top2[1] - top2[0] > 1e-3:
+            assert int(np.argmax(last)) == int(expect)
+        last = eng.step([int(expect)])[0]
+        np.testing.assert_allclose(last, z["greedy_logits"][i], rtol=0, atol=LOGIT_ATOL)
+
+
+def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path):
+    """The 0.1B architecture (14L, d=640, 16x40, ROSA 128, V=20480) on a short
+    batch, prefill then decode, against the float64 oracle."""
+    cfg = PRESETS["0.1b"]
+    weights = synth_weights(cfg, seed=0)
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, weights)
+    tokens = prompt_tokens(1, 2, 80, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=2, max_tokens=256)
+    got = eng.prefill(tokens, logits="all")
+    oracle = OracleModel(cfg.to_dict(), weights)
+    ref, state = oracle.forward(tokens)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=0, atol=LOGIT_ATOL)
+    nxt = uniform_tokens(2, 2, 3, cfg.vocab_size)
+    for t in range(3):
+        g = eng.step(nxt[:, t])
+        r, state = oracle.step(nxt[:, t], state)
+        np.testing.assert_allclose(g, r.numpy(), rtol=0, atol=LOGIT_ATOL)
+    blob = _states_from_blob(eng, [0, 1])
+    np.testing.assert_allclose(blob, state_to_blob(state), rtol=1e-4, atol=1e-4)
+
+
+def test_device_sampling():
+    torch.manual_seed(0)
+    logits = torch.randn(8, 20480, device="cuda") * 3
+    tokens = torch.empty(8, dtype=torch.int32, device="cuda")
+    sample_device(logits, tokens, 0.0, 32, seed=1, counter=0)
+    torch.cuda.synchronize()
+    assert torch.equal(tokens.long().cpu(), torch.argmax(logits, -1).cpu())
+    top = torch.topk(logits, 32, dim=-1).indices.cpu()
+    counts = torch.zeros(20480)
+    for c in range(200):
+        sample_device(logits, tokens, 1.0, 32, seed=1, counter=c)
+        torch.cuda.synchronize()
+        tk = tokens.long().cpu()
+        for b in range(8):
+            assert tk[b] in top[b]
+        counts[tk[0]] += 1
+    # Row 0: empirical frequencies follow softmax over its top-32 (loose bound).
+    p = torch.softmax(logits[0].cpu()[top[0]], 0)
+    emp = counts[top[0]] / 200
+    assert float((emp - p).abs().sum()) < 0.5

@@ -1,0 +1,161 @@
+// Memory-bound helper kernels of the model path (gfx950): embedding gather,
+// LayerNorm (+ gate), token shift, state bookkeeping, fills.
+//
+// Semantics: yufmusicgen/model.py:417 (embedding), nn.LayerNorm eps 1e-5
+// (model.py:89, :346-356, :391), token shift model.py:98-105 (sign of
+// x + (x - x_prev) * mu), the carried `previous` of model.py:197 and the
+// gated output norm of model.py:195-196.
+#include "common.h"
+#include "kernels.h"
+
+namespace yuf {
+namespace {
+
+constexpr int kWave = 64;
+
+// One wave per row; rows of width d <= 64 * kMaxPerLane.
+constexpr int kMaxPerLane = 32;
+
+template <int PER>
+__global__ void __launch_bounds__(256) layernorm_kernel(const float *x, int M, int d, const float *gamma,
+                                                        const float *beta, const float *gate, float *out) {
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= M) return;
+    const float *xr = x + (size_t)row * d;
+    float v[PER];
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = lane + e * kWave;
+        v[e] = c < d ? xr[c] : 0.0f;
+        sum += v[e];
+    }
+    const float mean = wave_sum(sum) / (float)d;
+    float sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = lane + e * kWave;
+        const float dv = c < d ? v[e] - mean : 0.0f;
+        sq = fmaf(dv, dv, sq);
+    }
+    const float rstd = rsqrtf(wave_sum(sq) / (float)d + 1e-5f);
+    float *orow = out + (size_t)row * d;
+    const float *grow = gate ? gate + (size_t)row * d : nullptr;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = lane + e * kWave;
+        if (c < d) {
+            float y = (v[e] - mean) * rstd * gamma[c] + beta[c];
+            if (grow) y *= grow[c];
+            orow[c] = y;
+        }
+    }
+}
+
+__global__ void embed_kernel(const int *tokens, int M, const float *table, int d, int vocab, float *out,
+                             int *bad) {
+    const int row = blockIdx.x;
+    if (row >= M) return;
+    const int tok = tokens[row];
+    const bool ok = tok >= 0 && tok < vocab;
+    if (!ok && threadIdx.x == 0 && bad) atomicOr(bad, 1);
+    const float *src = table + (size_t)(ok ? tok : 0) * d;
+    float *dst = out + (size_t)row * d;
+    for (int c = threadIdx.x; c < d; c += blockDim.x) dst[c] = ok ? src[c] : 0.0f;
+}
+
+__global__ void token_shift_kernel(const float *x, int Bn, int T, int d, const float *prev_state, const int *slot,
+                                   const float *mix6, float *out6, size_t out_stride) {
+    const size_t total = (size_t)Bn * T * d;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const size_t m = idx / d;
+        const int c = (int)(idx - m * d);
+        const int b = (int)(m / T), t = (int)(m - (size_t)b * T);
+        const float xv = x[idx];
+        const float pv = t > 0 ? x[idx - d] : prev_state[(size_t)(slot ? slot[b] : b) * d + c];
+        const float delta = xv - pv;
+#pragma unroll
+        for (int q = 0; q < 6; ++q) out6[q * out_stride + idx] = fmaf(delta, mix6[q * d + c], xv);
+    }
+}
+
+__global__ void save_prev_kernel(const float *x, int Bn, int T, int d, float *prev_state, const int *slot) {
+    const int b = blockIdx.x;
+    if (b >= Bn) return;
+    const float *src = x + ((size_t)b * T + T - 1) * d;
+    float *dst = prev_state + (size_t)(slot ? slot[b] : b) * d;
+    for (int c = threadIdx.x; c < d; c += blockDim.x) dst[c] = src[c];
+}
+
+__global__ void gather_last_kernel(const float *x, int Bn, int T, int d, float *out) {
+    const int b = blockIdx.x;
+    if (b >= Bn) return;
+    const float *src = x + ((size_t)b * T + T - 1) * d;
+    for (int c = threadIdx.x; c < d; c += blockDim.x) out[(size_t)b * d + c] = src[c];
+}
+
+__global__ void fill_kernel(float *p, size_t n, float value) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = value;
+}
+
+int grid_for(size_t n, int block) {
+    size_t g = (n + block - 1) / block;
+    return (int)(g < 65536 ? (g > 0 ? g : 1) : 65536);
+}
+
+}  // namespace
+
+hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, const float *beta, const float *gate,
+                            float *out, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    const int per = (d + kWave - 1) / kWave;
+    const dim3 grid((M + 3) / 4), block(256);
+    if (per <= 2) hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else if (per <= 4) hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else if (per <= 8) hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else if (per <= 16) hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else if (per <= kMaxPerLane)
+        hipLaunchKernelGGL(layernorm_kernel<kMaxPerLane>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(const int *tokens, int M, const float *table, int d, int vocab, float *out, int *bad,
+                        hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream, tokens, M, table, d, vocab, out, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_token_shift(const float *x, int Bn, int T, int d, const float *prev_state, const int *slot,
+                              const float *mix6, float *out6, size_t out_stride, hipStream_t stream) {
+    const size_t n = (size_t)Bn * T * d;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(token_shift_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, x, Bn, T, d, prev_state,
+                       slot, mix6, out6, out_stride);
+    return hipGetLastError();
+}
+
+hipError_t launch_save_prev(const float *x, int Bn, int T, int d, float *prev_state, const int *slot,
+                            hipStream_t stream) {
+    if (Bn <= 0 || T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(save_prev_kernel, dim3(Bn), dim3(256), 0, stream, x, Bn, T, d, prev_state, slot);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_last(const float *x, int Bn, int T, int d, float *out, hipStream_t stream) {
+    if (Bn <= 0 || T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gather_last_kernel, dim3(Bn), dim3(256), 0, stream, x, Bn, T, d, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill(float *p, size_t n, float value, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, p, n, value);
+    return hipGetLastError();
+}
+
+}  // namespace yuf

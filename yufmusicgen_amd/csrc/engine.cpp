@@ -1,0 +1,597 @@
+// The inference engine behind the C ABI: device-resident weights, per-stream
+// recurrent state in HBM, batched prefill and multi-stream decode.
+//
+// Replaces the reference's Vulkan `Model` (vulkan/src/compute/model.rs:24-65,
+// op order :425-757) and the Python forward/step (yufmusicgen/model.py:97-445):
+//   embedding -> per layer [LN_t -> token shift -> r/k/v/w/a/g projections ->
+//   WKV-7 scan -> LN_out * g -> W_o (+res) -> LN_r -> ROSA c/w/rho -> ROSA scan
+//   -> W_out (+res) -> LN_f -> FFN in/gate (silu * gate) -> W_ffn_out (+res)]
+//   -> final LN -> tied LM head.
+// State per stream and layer: previous normed input [d], WKV state [H, N, N]
+// (row = value index), ROSA memory [D] -- the BlockState of model.py:29-38.
+//
+// Differences by design: prefill is one batched pass per T-chunk instead of a
+// per-token loop (generation.rs:176-185); any number of streams share the
+// engine through state slots; `previous` is part of the state that
+// yuf_state_reset clears (the Rust reset leaves it stale, mod.rs:706-724).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/yuf_engine.h"
+#include "checkpoint.h"
+#include "common.h"
+#include "kernels.h"
+
+namespace yuf {
+
+namespace {
+
+struct LayerW {
+    const float *ln_t_w, *ln_t_b, *mix6;
+    const float *w_r, *w_k, *w_v, *w_o;
+    const float *w1t, *w2t, *a1t, *a2t, *g1t, *g2t;  // low-rank pairs as [out, in]
+    const float *w0, *a0, *k_k, *k_a;
+    const float *ln_o_w, *ln_o_b, *ln_r_w, *ln_r_b;
+    const float *rosa_w3, *rosa_b3, *rosa_hh, *rosa_decay, *rosa_out;
+    const float *ln_f_w, *ln_f_b, *ffn_cat, *ffn_out;
+};
+
+struct DeviceBuf {
+    void *p = nullptr;
+    ~DeviceBuf() {
+        if (p) (void)hipFree(p);
+    }
+};
+
+}  // namespace
+
+struct Engine {
+    ModelShape s;
+    int max_streams = 0, max_tokens = 0;
+    hipStream_t stream = nullptr;
+    DeviceBuf weights, state, work, io;
+    std::vector<LayerW> layers;
+    const float *emb = nullptr, *ln_fin_w = nullptr, *ln_fin_b = nullptr, *head = nullptr;
+    // state arrays, [layer][slot][...]
+    float *st_prev = nullptr, *st_wkv = nullptr, *st_rosa = nullptr;
+    // workspace (sized for max_tokens rows)
+    float *h = nullptr, *xn = nullptr, *mix = nullptr, *r = nullptr, *k = nullptr, *v = nullptr, *wr = nullptr,
+          *al = nullptr, *g = nullptr, *lr = nullptr, *y = nullptr, *z = nullptr, *rosa3 = nullptr, *rread = nullptr,
+          *ffn = nullptr, *hl = nullptr;
+    int *slots_dev = nullptr, *tokens_dev = nullptr, *bad_dev = nullptr;
+    int *slots_host = nullptr;  // pinned
+    std::vector<int> last_slots;
+    // Device staging for the host-buffer entry points (grown on demand).
+    DeviceBuf host_tokens, host_logits;
+    size_t host_tokens_cap = 0, host_logits_cap = 0;
+
+    ~Engine() {
+        if (stream) {
+            (void)hipStreamSynchronize(stream);
+            (void)hipStreamDestroy(stream);
+        }
+        if (slots_host) (void)hipHostFree(slots_host);
+    }
+
+    size_t wkv_floats() const { return (size_t)s.heads * s.head_size * s.head_size; }
+    size_t state_floats() const { return (size_t)s.layers * (s.d + wkv_floats() + s.rosa); }
+};
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(YUF_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define ENG_TRY(expr, what)                                  \
+    do {                                                     \
+        hipError_t e_ = (expr);                              \
+        if (e_ != hipSuccess) return hip_fail(e_, what);     \
+    } while (0)
+
+// Host-side weight preparation: the device layout the kernels want.
+int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<size_t> &offsets, std::string &err) {
+    const ModelShape &s = ck.shape;
+    const long long d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4LL * s.d;
+    auto append = [&](const float *src, size_t n) {
+        // Keep every tensor 256-byte aligned for vector loads.
+        size_t off = (host.size() + 63) & ~size_t(63);
+        host.resize(off + n);
+        std::memcpy(host.data() + off, src, n * sizeof(float));
+        offsets.push_back(off);
+    };
+    auto get = [&](const std::string &name, std::vector<long long> dims) -> const float * {
+        return ck.tensor(name, dims, err);
+    };
+    auto transposed = [&](const float *src, long long rows, long long cols) {
+        std::vector<float> t((size_t)(rows * cols));
+        for (long long i = 0; i < rows; ++i)
+            for (long long j = 0; j < cols; ++j) t[(size_t)(j * rows + i)] = src[i * cols + j];
+        return t;
+    };
+    const float *e = get("token_embedding.weight", {V, d});
+    if (!e) return YUF_ERR_FORMAT;
+    append(e, (size_t)(V * d));
+    const float *head = e;
+    if (!s.tie) {
+        head = get("lm_head.weight", {V, d});
+        if (!head) return YUF_ERR_FORMAT;
+    }
+    append(head, (size_t)(V * d));
+    for (const char *n : {"final_norm.weight", "final_norm.bias"}) {
+        const float *p = get(n, {d});
+        if (!p) return YUF_ERR_FORMAT;
+        append(p, (size_t)d);
+    }
+    for (int l = 0; l < s.layers; ++l) {
+        const std::string pre = "blocks." + std::to_string(l) + ".";
+        auto vec = [&](const std::string &n) -> bool {
+            const float *p = get(pre + n, {n.find("rosa.") == 0 ? D : d});
+            if (!p) return false;
+            append(p, (size_t)(n.find("rosa.") == 0 ? D : d));
+            return true;
+        };
+        auto mat = [&](const std::string &n, long long rows, long long cols) -> bool {
+            const float *p = get(pre + n, {rows, cols});
+            if (!p) return false;
+            append(p, (size_t)(rows * cols));
+            return true;
+        };
+        auto mat_t = [&](const std::string &n, long long rows, long long cols) -> bool {
+            const float *p = get(pre + n, {rows, cols});
+            if (!p) return false;
+            std::vector<float> t = transposed(p, rows, cols);
+            append(t.data(), t.size());
+            return true;
+        };
+        if (!vec("norm_time.weight") || !vec("norm_time.bias")) return YUF_ERR_FORMAT;
+        {
+            std::vector<float> mix6((size_t)(6 * d));
+            const char *names[6] = {"mix_r", "mix_w", "mix_k", "mix_v", "mix_a", "mix_g"};
+            for (int c = 0; c < 6; ++c) {
+                const float *p = get(pre + "time_mix." + names[c], {d});
+                if (!p) return YUF_ERR_FORMAT;
+                std::memcpy(mix6.data() + c * d, p, d * sizeof(float));
+            }
+            append(mix6.data(), mix6.size());
+        }
+        if (!mat("time_mix.receptance.weight", d, d) || !mat("time_mix.key.weight", d, d) ||
+            !mat("time_mix.value.weight", d, d) || !mat("time_mix.output.weight", d, d))
+            return YUF_ERR_FORMAT;
+        if (!mat_t("time_mix.w1", d, L) || !mat_t("time_mix.w2", L, d) || !mat_t("time_mix.a1", d, L) ||
+            !mat_t("time_mix.a2", L, d) || !mat_t("time_mix.g1", d, L) || !mat_t("time_mix.g2", L, d))
+            return YUF_ERR_FORMAT;
+        if (!vec("time_mix.w0") || !vec("time_mix.a0") || !vec("time_mix.k_k") || !vec("time_mix.k_a"))
+            return YUF_ERR_FORMAT;
+        if (!vec("time_mix.out_norm.weight") || !vec("time_mix.out_norm.bias") || !vec("norm_rosa.weight") ||
+            !vec("norm_rosa.bias"))
+            return YUF_ERR_FORMAT;
+        {
+            std::vector<float> w3((size_t)(3 * D * d)), b3((size_t)(3 * D));
+            const char *names[3] = {"rosa.input", "rosa.write_gate", "rosa.read_gate"};
+            for (int c = 0; c < 3; ++c) {
+                const float *w = get(pre + names[c] + ".weight", {D, d});
+                const float *b = get(pre + names[c] + ".bias", {D});
+                if (!w || !b) return YUF_ERR_FORMAT;
+                std::memcpy(w3.data() + c * D * d, w, (size_t)(D * d) * sizeof(float));
+                std::memcpy(b3.data() + c * D, b, (size_t)D * sizeof(float));
+            }
+            append(w3.data(), w3.size());
+            append(b3.data(), b3.size());
+        }
+        if (!vec("rosa.householder") || !vec("rosa.decay") || !mat("rosa.output.weight", d, D)) return YUF_ERR_FORMAT;
+        if (!vec("norm_ffn.weight") || !vec("norm_ffn.bias")) return YUF_ERR_FORMAT;
+        {
+            const float *wi = get(pre + "ffn_in.weight", {hid, d});
+            const float *wg = get(pre + "ffn_gate.weight", {hid, d});
+            if (!wi || !wg) return YUF_ERR_FORMAT;
+            if (hid % 32 != 0) {
+                err = "ffn hidden width must be a multiple of 32";
+                return YUF_ERR_FORMAT;
+            }
+            // Rows in blocks of 64: 32 rows of ffn_in, then the same 32 of ffn_gate.
+            std::vector<float> cat((size_t)(2 * hid * d));
+            for (long long q = 0; q < hid / 32; ++q) {
+                std::memcpy(cat.data() + (size_t)(q * 64) * d, wi + (size_t)(q * 32) * d, 32 * d * sizeof(float));
+                std::memcpy(cat.data() + (size_t)(q * 64 + 32) * d, wg + (size_t)(q * 32) * d, 32 * d * sizeof(float));
+            }
+            append(cat.data(), cat.size());
+        }
+        if (!mat("ffn_out.weight", d, hid)) return YUF_ERR_FORMAT;
+    }
+    return YUF_OK;
+}
+
+template <typename T>
+T *carve(char *&cursor, size_t count) {
+    T *p = reinterpret_cast<T *>(cursor);
+    cursor += ((count * sizeof(T) + 255) / 256) * 256;
+    return p;
+}
+
+int gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C, int ldc,
+         const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr, int ldr = 0,
+         bool silu_pair = false) {
+    GemmParams p;
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.C = C; p.ldc = ldc;
+    p.bias = bias; p.act = act; p.residual = residual; p.ldr = ldr; p.silu_pair = silu_pair;
+    ENG_TRY(launch_gemm(p, e.stream), "gemm");
+    return YUF_OK;
+}
+
+// One forward pass over n streams x Tc tokens already in e.tokens_dev / e.slots_dev.
+// logits: LAST -> [n, V] at `logits`; ALL -> row (b, t) at logits + (b * row_stride_T + t0 + t) * V.
+int forward_pass(Engine &e, int n, int Tc, float *logits, int mode, int row_stride_T, int t0) {
+    const ModelShape &s = e.s;
+    const int M = n * Tc, d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4 * s.d;
+    const size_t plane = (size_t)e.max_tokens * d;
+    hipStream_t st = e.stream;
+    ENG_TRY(launch_embed(e.tokens_dev, M, e.emb, d, V, e.h, e.bad_dev, st), "embed");
+    for (int l = 0; l < s.layers; ++l) {
+        const LayerW &w = e.layers[l];
+        float *prev = e.st_prev + (size_t)l * e.max_streams * d;
+        float *wkv = e.st_wkv + (size_t)l * e.max_streams * e.wkv_floats();
+        float *ros = e.st_rosa + (size_t)l * e.max_streams * D;
+        // TimeMix
+        ENG_TRY(launch_layernorm(e.h, M, d, w.ln_t_w, w.ln_t_b, nullptr, e.xn, st), "ln_time");
+        ENG_TRY(launch_token_shift(e.xn, n, Tc, d, prev, e.slots_dev, w.mix6, e.mix, plane, st), "token_shift");
+        ENG_TRY(launch_save_prev(e.xn, n, Tc, d, prev, e.slots_dev, st), "save_prev");
+        const float *mr = e.mix, *mw = e.mix + plane, *mk = e.mix + 2 * plane, *mv = e.mix + 3 * plane,
+                    *ma = e.mix + 4 * plane, *mg = e.mix + 5 * plane;
+        int rc;
+        if ((rc = gemm(e, M, d, d, mr, d, w.w_r, d, e.r, d)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, d, d, mk, d, w.w_k, d, e.k, d)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, d, d, mv, d, w.w_v, d, e.v, d)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, L, d, mw, d, w.w1t, d, e.lr, L, nullptr, ACT_TANH)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, d, L, e.lr, L, w.w2t, L, e.wr, d, w.w0)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, L, d, ma, d, w.a1t, d, e.lr, L)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, d, L, e.lr, L, w.a2t, L, e.al, d, w.a0, ACT_SIGMOID)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, L, d, mg, d, w.g1t, d, e.lr, L)) != YUF_OK) return rc;
+        if ((rc = gemm(e, M, d, L, e.lr, L, w.g2t, L, e.g, d, nullptr, ACT_SIGMOID)) != YUF_OK) return rc;
+        WkvParams wp;
+        wp.B = n; wp.T = Tc; wp.H = s.heads;
+        wp.r = e.r; wp.w = e.wr; wp.k = e.k; wp.v = e.v; wp.a = e.al;
+        wp.k_k = w.k_k; wp.k_a = w.k_a;
+        wp.state_in = wkv; wp.state_out = wkv; wp.slot = e.slots_dev; wp.y = e.y;
+        ENG_TRY(launch_wkv7(wp, s.head_size, true, st), "wkv7");
+        ENG_TRY(launch_layernorm(e.y, M, d, w.ln_o_w, w.ln_o_b, e.g, e.z, st), "ln_out");
+        if ((rc = gemm(e, M, d, d, e.z, d, w.w_o, d, e.h, d, nullptr, ACT_NONE, e.h, d)) != YUF_OK) return rc;
+        // ROSA
+        ENG_TRY(launch_layernorm(e.h, M, d, w.ln_r_w, w.ln_r_b, nullptr, e.xn, st), "ln_rosa");
+        if ((rc = gemm(e, M, 3 * D, d, e.xn, d, w.rosa_w3, d, e.rosa3, 3 * D, w.rosa_b3)) != YUF_OK) return rc;
+        RosaParams rp;
+        rp.B = n; rp.T = Tc; rp.D = D; rp.ld = 3 * D;
+        rp.cand = e.rosa3; rp.write = e.rosa3 + D; rp.read_raw = e.rosa3 + 2 * D;
+        rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
+        rp.memory_in = ros; rp.memory_out = ros; rp.slot = e.slots_dev; rp.read_out = e.rread;
+        ENG_TRY(launch_rosa(rp, st), "rosa");
+        if ((rc = gemm(e, M, d, D, e.rread, D, w.rosa_out, D, e.h, d, nullptr, ACT_NONE, e.h, d)) != YUF_OK) return rc;
+        // FFN
+        ENG_TRY(launch_layernorm(e.h, M, d, w.ln_f_w, w.ln_f_b, nullptr, e.xn, st), "ln_ffn");
+        if ((rc = gemm(e, M, 2 * hid, d, e.xn, d, w.ffn_cat, d, e.ffn, hid, nullptr, ACT_NONE, nullptr, 0, true)) != YUF_OK)
+            return rc;
+        if ((rc = gemm(e, M, d, hid, e.ffn, hid, w.ffn_out, hid, e.h, d, nullptr, ACT_NONE, e.h, d)) != YUF_OK)
+            return rc;
+    }
+    if (mode == YUF_LOGITS_LAST) {
+        ENG_TRY(launch_gather_last(e.h, n, Tc, d, e.hl, st), "gather_last");
+        ENG_TRY(launch_layernorm(e.hl, n, d, e.ln_fin_w, e.ln_fin_b, nullptr, e.xn, st), "ln_final");
+        return gemm(e, n, V, d, e.xn, d, e.head, d, logits, V);
+    }
+    if (mode == YUF_LOGITS_ALL) {
+        ENG_TRY(launch_layernorm(e.h, M, d, e.ln_fin_w, e.ln_fin_b, nullptr, e.xn, st), "ln_final");
+        if (row_stride_T == Tc && t0 == 0) return gemm(e, M, V, d, e.xn, d, e.head, d, logits, V);
+        for (int b = 0; b < n; ++b) {
+            int rc = gemm(e, Tc, V, d, e.xn + (size_t)b * Tc * d, d, e.head, d,
+                          logits + ((size_t)b * row_stride_T + t0) * V, V);
+            if (rc != YUF_OK) return rc;
+        }
+    }
+    return YUF_OK;
+}
+
+int check_slots(const Engine &e, int n, const int32_t *slots) {
+    if (n <= 0) return fail(YUF_ERR_INVALID, "n must be positive");
+    if (n > e.max_streams) return fail(YUF_ERR_RANGE, "more streams than the engine's max_streams");
+    if (!slots) return fail(YUF_ERR_INVALID, "null slots");
+    std::set<int> seen;
+    for (int i = 0; i < n; ++i) {
+        if (slots[i] < 0 || slots[i] >= e.max_streams)
+            return fail(YUF_ERR_RANGE, "stream slot " + std::to_string(slots[i]) + " out of range");
+        if (!seen.insert(slots[i]).second) return fail(YUF_ERR_INVALID, "duplicate stream slot in one call");
+    }
+    return YUF_OK;
+}
+
+int upload_slots(Engine &e, int n, const int32_t *slots) {
+    std::vector<int> cur(slots, slots + n);
+    if (cur == e.last_slots) return YUF_OK;
+    std::memcpy(e.slots_host, slots, n * sizeof(int));
+    ENG_TRY(hipMemcpyAsync(e.slots_dev, e.slots_host, n * sizeof(int), hipMemcpyHostToDevice, e.stream), "slots upload");
+    ENG_TRY(hipStreamSynchronize(e.stream), "slots upload sync");
+    e.last_slots = cur;
+    return YUF_OK;
+}
+
+// Prefill n x T tokens (device pointer), splitting T into chunks of at most max_tokens / n.
+int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logits_dev, int mode) {
+    const int tc_max = std::max(1, e.max_tokens / n);
+    if (n > e.max_tokens) return fail(YUF_ERR_RANGE, "n exceeds max_tokens");
+    for (int t0 = 0; t0 < T; t0 += tc_max) {
+        const int tc = std::min(tc_max, T - t0);
+        // Gather this chunk's token ids into [n, tc] rows.
+        if (tc == T) {
+            ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * T * sizeof(int), hipMemcpyDeviceToDevice, e.stream),
+                    "tokens copy");
+        } else {
+            ENG_TRY(hipMemcpy2DAsync(e.tokens_dev, (size_t)tc * sizeof(int), tokens_dev + t0, (size_t)T * sizeof(int),
+                                     (size_t)tc * sizeof(int), n, hipMemcpyDeviceToDevice, e.stream),
+                    "tokens copy");
+        }
+        const bool last_chunk = t0 + tc >= T;
+        const int chunk_mode = mode == YUF_LOGITS_ALL ? YUF_LOGITS_ALL : (last_chunk ? mode : YUF_LOGITS_NONE);
+        int rc = forward_pass(e, n, tc, logits_dev, chunk_mode, T, t0);
+        if (rc != YUF_OK) return rc;
+    }
+    return YUF_OK;
+}
+
+}  // namespace
+
+}  // namespace yuf
+
+// --------------------------------------------------------------------- C ABI
+struct yuf_engine {
+    yuf::Engine e;
+};
+
+using yuf::fail;
+
+extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_tokens, yuf_engine **out) {
+    using namespace yuf;
+    if (!ckpt || !out) return fail(YUF_ERR_INVALID, "yuf_engine_create: null argument");
+    *out = nullptr;
+    if (max_streams < 1 || max_tokens < 1) return fail(YUF_ERR_INVALID, "max_streams and max_tokens must be >= 1");
+    const Checkpoint &ck = checkpoint_of(ckpt);
+    const ModelShape &s = ck.shape;
+    if (!wkv7_supported(s.head_size))
+        return fail(YUF_ERR_INVALID, "head_size " + std::to_string(s.head_size) + " has no scan kernel");
+    if (s.d > 64 * 32) return fail(YUF_ERR_INVALID, "d_model above 2048 is not supported");
+    if (s.rosa > 1024) return fail(YUF_ERR_INVALID, "rosa_size above 1024 is not supported");
+    std::unique_ptr<yuf_engine> h(new (std::nothrow) yuf_engine());
+    if (!h) return fail(YUF_ERR_OOM, "host allocation failed");
+    Engine &e = h->e;
+    e.s = s;
+    e.max_streams = max_streams;
+    e.max_tokens = max_tokens;
+
+    std::vector<float> host;
+    std::vector<size_t> offs;
+    std::string err;
+    try {
+        int rc = build_weights(ck, host, offs, err);
+        if (rc != YUF_OK) return fail(rc, err);
+    } catch (const std::bad_alloc &) {
+        return fail(YUF_ERR_OOM, "out of host memory preparing weights");
+    }
+    ENG_TRY(hipStreamCreateWithFlags(&e.stream, hipStreamNonBlocking), "stream create");
+    ENG_TRY(hipMalloc(&e.weights.p, host.size() * sizeof(float)), "weights alloc");
+    ENG_TRY(hipMemcpy(e.weights.p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice), "weights upload");
+    const float *base = static_cast<const float *>(e.weights.p);
+    size_t oi = 0;
+    auto nxt = [&]() { return base + offs[oi++]; };
+    e.emb = nxt();
+    e.head = nxt();
+    e.ln_fin_w = nxt();
+    e.ln_fin_b = nxt();
+    e.layers.resize(s.layers);
+    for (int l = 0; l < s.layers; ++l) {
+        LayerW &w = e.layers[l];
+        w.ln_t_w = nxt(); w.ln_t_b = nxt(); w.mix6 = nxt();
+        w.w_r = nxt(); w.w_k = nxt(); w.w_v = nxt(); w.w_o = nxt();
+        w.w1t = nxt(); w.w2t = nxt(); w.a1t = nxt(); w.a2t = nxt(); w.g1t = nxt(); w.g2t = nxt();
+        w.w0 = nxt(); w.a0 = nxt(); w.k_k = nxt(); w.k_a = nxt();
+        w.ln_o_w = nxt(); w.ln_o_b = nxt(); w.ln_r_w = nxt(); w.ln_r_b = nxt();
+        w.rosa_w3 = nxt(); w.rosa_b3 = nxt(); w.rosa_hh = nxt(); w.rosa_decay = nxt(); w.rosa_out = nxt();
+        w.ln_f_w = nxt(); w.ln_f_b = nxt(); w.ffn_cat = nxt(); w.ffn_out = nxt();
+    }
+
+    // State: [layer][slot][...] for each of prev, wkv, rosa.
+    const size_t n_prev = (size_t)s.layers * max_streams * s.d;
+    const size_t n_wkv = (size_t)s.layers * max_streams * e.wkv_floats();
+    const size_t n_rosa = (size_t)s.layers * max_streams * s.rosa;
+    const size_t state_bytes = (n_prev + n_wkv + n_rosa) * sizeof(float) + 3 * 256;
+    ENG_TRY(hipMalloc(&e.state.p, state_bytes), "state alloc");
+    {
+        char *cur = static_cast<char *>(e.state.p);
+        e.st_prev = carve<float>(cur, n_prev);
+        e.st_wkv = carve<float>(cur, n_wkv);
+        e.st_rosa = carve<float>(cur, n_rosa);
+    }
+    ENG_TRY(hipMemsetAsync(e.state.p, 0, state_bytes, e.stream), "state clear");
+
+    // Workspace.
+    const size_t Mx = (size_t)max_tokens, d = s.d;
+    const size_t sizes[] = {Mx * d, Mx * d, 6 * Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d,
+                            Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
+                            (size_t)max_streams * d};
+    size_t total = 0;
+    for (size_t z : sizes) total += ((z * sizeof(float) + 255) / 256) * 256;
+    ENG_TRY(hipMalloc(&e.work.p, total), "workspace alloc");
+    {
+        char *cur = static_cast<char *>(e.work.p);
+        float **dst[] = {&e.h, &e.xn, &e.mix, &e.r, &e.k, &e.v, &e.wr, &e.al, &e.g, &e.lr, &e.y, &e.z, &e.rosa3,
+                         &e.rread, &e.ffn, &e.hl};
+        for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
+    }
+    const size_t io_bytes = 256 * 3 + (size_t)(max_streams + max_tokens + 1) * sizeof(int);
+    ENG_TRY(hipMalloc(&e.io.p, io_bytes), "io alloc");
+    {
+        char *cur = static_cast<char *>(e.io.p);
+        e.slots_dev = carve<int>(cur, max_streams);
+        e.tokens_dev = carve<int>(cur, max_tokens);
+        e.bad_dev = carve<int>(cur, 1);
+    }
+    ENG_TRY(hipHostMalloc(reinterpret_cast<void **>(&e.slots_host), max_streams * sizeof(int)), "pinned alloc");
+    ENG_TRY(hipMemsetAsync(e.bad_dev, 0, sizeof(int), e.stream), "flag clear");
+    ENG_TRY(hipStreamSynchronize(e.stream), "engine init sync");
+    *out = h.release();
+    return YUF_OK;
+}
+
+extern "C" void yuf_engine_destroy(yuf_engine *eng) { delete eng; }
+
+extern "C" int yuf_engine_config(const yuf_engine *eng, yuf_model_config *out) {
+    if (!eng || !out) return fail(YUF_ERR_INVALID, "yuf_engine_config: null argument");
+    yuf::fill_config(eng->e.s, *out);
+    return YUF_OK;
+}
+
+extern "C" void *yuf_engine_stream(yuf_engine *eng) { return eng ? static_cast<void *>(eng->e.stream) : nullptr; }
+
+namespace {
+
+int check_tokens_host(const yuf::Engine &e, const int32_t *tokens, size_t count) {
+    if (!tokens) return fail(YUF_ERR_INVALID, "null tokens");
+    for (size_t i = 0; i < count; ++i)
+        if (tokens[i] < 0 || tokens[i] >= e.s.vocab)
+            return fail(YUF_ERR_RANGE, "token id " + std::to_string(tokens[i]) + " out of range [0, " +
+                                           std::to_string(e.s.vocab) + ")");
+    return YUF_OK;
+}
+
+}  // namespace
+
+extern "C" int yuf_prefill_device(yuf_engine *eng, int n, const int32_t *slots, int T, const int32_t *tokens_dev,
+                                  float *logits_dev, int logits_mode) {
+    using namespace yuf;
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    Engine &e = eng->e;
+    int rc = check_slots(e, n, slots);
+    if (rc != YUF_OK) return rc;
+    if (T < 0) return fail(YUF_ERR_INVALID, "negative T");
+    if (T == 0) return YUF_OK;
+    if (logits_mode < YUF_LOGITS_NONE || logits_mode > YUF_LOGITS_ALL) return fail(YUF_ERR_INVALID, "bad logits mode");
+    if (!tokens_dev || (logits_mode != YUF_LOGITS_NONE && !logits_dev)) return fail(YUF_ERR_INVALID, "null buffer");
+    if ((rc = upload_slots(e, n, slots)) != YUF_OK) return rc;
+    return prefill_impl(e, n, T, tokens_dev, logits_dev, logits_mode);
+}
+
+extern "C" int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T, const int32_t *tokens, float *logits,
+                           int logits_mode) {
+    using namespace yuf;
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    Engine &e = eng->e;
+    int rc = check_slots(e, n, slots);
+    if (rc != YUF_OK) return rc;
+    if (T < 0) return fail(YUF_ERR_INVALID, "negative T");
+    if (T == 0) return YUF_OK;
+    if (logits_mode < YUF_LOGITS_NONE || logits_mode > YUF_LOGITS_ALL) return fail(YUF_ERR_INVALID, "bad logits mode");
+    if ((rc = check_tokens_host(e, tokens, (size_t)n * T)) != YUF_OK) return rc;
+    if (logits_mode != YUF_LOGITS_NONE && !logits) return fail(YUF_ERR_INVALID, "null logits");
+    const size_t n_logits =
+        logits_mode == YUF_LOGITS_ALL ? (size_t)n * T * e.s.vocab : (logits_mode == YUF_LOGITS_LAST ? (size_t)n * e.s.vocab : 0);
+    const size_t n_tok = (size_t)n * T;
+    if (n_tok > e.host_tokens_cap) {
+        if (e.host_tokens.p) ENG_TRY(hipFree(e.host_tokens.p), "token buffer");
+        e.host_tokens.p = nullptr;
+        e.host_tokens_cap = 0;
+        ENG_TRY(hipMalloc(&e.host_tokens.p, n_tok * sizeof(int)), "token buffer");
+        e.host_tokens_cap = n_tok;
+    }
+    if (n_logits > e.host_logits_cap) {
+        if (e.host_logits.p) ENG_TRY(hipFree(e.host_logits.p), "logits buffer");
+        e.host_logits.p = nullptr;
+        e.host_logits_cap = 0;
+        ENG_TRY(hipMalloc(&e.host_logits.p, n_logits * sizeof(float)), "logits buffer");
+        e.host_logits_cap = n_logits;
+    }
+    ENG_TRY(hipMemcpyAsync(e.host_tokens.p, tokens, n_tok * sizeof(int), hipMemcpyHostToDevice, e.stream),
+            "tokens upload");
+    if ((rc = upload_slots(e, n, slots)) != YUF_OK) return rc;
+    if ((rc = prefill_impl(e, n, T, static_cast<int *>(e.host_tokens.p), static_cast<float *>(e.host_logits.p),
+                           logits_mode)) != YUF_OK)
+        return rc;
+    if (n_logits)
+        ENG_TRY(hipMemcpyAsync(logits, e.host_logits.p, n_logits * sizeof(float), hipMemcpyDeviceToHost, e.stream),
+                "logits download");
+    int bad = 0;
+    ENG_TRY(hipMemcpyAsync(&bad, e.bad_dev, sizeof(int), hipMemcpyDeviceToHost, e.stream), "flag read");
+    ENG_TRY(hipStreamSynchronize(e.stream), "prefill sync");
+    if (bad) {
+        ENG_TRY(hipMemsetAsync(e.bad_dev, 0, sizeof(int), e.stream), "flag clear");
+        return fail(YUF_ERR_RANGE, "a device-side token id was out of range (its embedding was zeroed)");
+    }
+    return YUF_OK;
+}
+
+extern "C" int yuf_step_device(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens_dev,
+                               float *logits_dev) {
+    return yuf_prefill_device(eng, n, slots, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
+}
+
+extern "C" int yuf_step(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens, float *logits) {
+    return yuf_prefill(eng, n, slots, 1, tokens, logits, YUF_LOGITS_LAST);
+}
+
+extern "C" int yuf_state_reset(yuf_engine *eng, int slot) {
+    using namespace yuf;
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    Engine &e = eng->e;
+    if (slot < -1 || slot >= e.max_streams) return fail(YUF_ERR_RANGE, "slot out of range");
+    const int first = slot < 0 ? 0 : slot, count = slot < 0 ? e.max_streams : 1;
+    for (int l = 0; l < e.s.layers; ++l) {
+        struct { float *base; size_t per; } parts[3] = {
+            {e.st_prev + (size_t)l * e.max_streams * e.s.d, (size_t)e.s.d},
+            {e.st_wkv + (size_t)l * e.max_streams * e.wkv_floats(), e.wkv_floats()},
+            {e.st_rosa + (size_t)l * e.max_streams * e.s.rosa, (size_t)e.s.rosa}};
+        for (auto &p : parts)
+            ENG_TRY(launch_fill(p.base + (size_t)first * p.per, (size_t)count * p.per, 0.0f, e.stream), "state reset");
+    }
+    ENG_TRY(hipStreamSynchronize(e.stream), "state reset sync");
+    return YUF_OK;
+}
+
+extern "C" size_t yuf_state_size(const yuf_engine *eng) {
+    return eng ? eng->e.state_floats() * sizeof(float) : 0;
+}
+
+namespace {
+int state_copy(yuf::Engine &e, int slot, float *host, bool save) {
+    using namespace yuf;
+    if (slot < 0 || slot >= e.max_streams) return fail(YUF_ERR_RANGE, "slot out of range");
+    if (!host) return fail(YUF_ERR_INVALID, "null state buffer");
+    size_t off = 0;
+    for (int l = 0; l < e.s.layers; ++l) {
+        struct { float *dev; size_t n; } parts[3] = {
+            {e.st_prev + ((size_t)l * e.max_streams + slot) * e.s.d, (size_t)e.s.d},
+            {e.st_wkv + ((size_t)l * e.max_streams + slot) * e.wkv_floats(), e.wkv_floats()},
+            {e.st_rosa + ((size_t)l * e.max_streams + slot) * e.s.rosa, (size_t)e.s.rosa}};
+        for (auto &p : parts) {
+            if (save)
+                ENG_TRY(hipMemcpyAsync(host + off, p.dev, p.n * sizeof(float), hipMemcpyDeviceToHost, e.stream), "state save");
+            else
+                ENG_TRY(hipMemcpyAsync(p.dev, host + off, p.n * sizeof(float), hipMemcpyHostToDevice, e.stream), "state load");
+            off += p.n;
+        }
+    }
+    ENG_TRY(hipStreamSynchronize(e.stream), "state copy sync");
+    return YUF_OK;
+}
+}  // namespace
+
+extern "C" int yuf_state_save(yuf_engine *eng, int slot, void *host_buf) {
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    return state_copy(eng->e, slot, static_cast<float *>(host_buf), true);
+}
+
+extern "C" int yuf_state_load(yuf_engine *eng, int slot, const void *host_buf) {
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    return state_copy(eng->e, slot, static_cast<float *>(const_cast<void *>(host_buf)), false);
+}

@@ -1,0 +1,90 @@
+// Internal launch interfaces of the HIP kernels (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace yuf {
+
+// ----------------------------------------------------------------- WKV-7 scan
+struct WkvParams {
+    int B = 0, T = 0, H = 0;
+    // Per-token inputs, [B, T, H, N] contiguous.
+    const float *r = nullptr, *w = nullptr, *k = nullptr, *v = nullptr;
+    const float *a = nullptr, *b = nullptr;
+    // Fused-prep mode (the model path): `a` holds the post-sigmoid gate alpha,
+    // `k` the raw key; kk = normalize(k * k_k) per head, a = -kk, b = kk * alpha,
+    // k_hat = k * (1 + (alpha - 1) * k_a)  (yufmusicgen/model.py:114-122).
+    const float *k_k = nullptr, *k_a = nullptr;  // [H * N]
+    // State [slots, H, N, N]; stream b uses slot `slot[b]` (slot == nullptr: b).
+    const float *state_in = nullptr;
+    float *state_out = nullptr;
+    const int *slot = nullptr;
+    float *y = nullptr;  // [B, T, H, N]
+};
+bool wkv7_supported(int N);
+hipError_t launch_wkv7(const WkvParams &p, int N, bool prep, hipStream_t stream);
+
+// ------------------------------------------------------------------ ROSA scan
+struct RosaParams {
+    int B = 0, T = 0, D = 0;
+    // Pre-activations; element (b, t, c) at base[(b * T + t) * ld + c].
+    const float *cand = nullptr, *write = nullptr, *read_raw = nullptr;
+    int ld = 0;
+    const float *decay = nullptr, *direction = nullptr;  // [D]
+    // Model path: derive lambda = sigmoid(decay_param), u = normalize(householder).
+    bool raw_params = false;
+    const float *memory_in = nullptr;
+    float *memory_out = nullptr;
+    const int *slot = nullptr;
+    float *read_out = nullptr;  // [(b * T + t) * D + c]
+};
+hipError_t launch_rosa(const RosaParams &p, hipStream_t stream);
+
+// ----------------------------------------------------------------------- GEMM
+// C[m, n] = epilogue( sum_k A[m, k] * W[n, k] )   (nn.Linear: y = x W^T)
+enum GemmAct : int { ACT_NONE = 0, ACT_TANH = 1, ACT_SIGMOID = 2 };
+struct GemmParams {
+    int M = 0, N = 0, K = 0;
+    const float *A = nullptr;
+    int lda = 0;
+    const float *W = nullptr;
+    int ldw = 0;
+    float *C = nullptr;
+    int ldc = 0;
+    const float *bias = nullptr;      // [N] added before the activation
+    int act = ACT_NONE;
+    const float *residual = nullptr;  // [M, ldr] added after the activation (may alias C)
+    int ldr = 0;
+    // Paired SiLU-gate output: W rows come in blocks of 64 = 32 "in" rows then
+    // 32 "gate" rows; C[m, 32 q + c] = silu(in) * gate.  N counts W rows.
+    bool silu_pair = false;
+};
+hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
+
+// ---------------------------------------------------------------- elementwise
+hipError_t launch_embed(const int *tokens, int M, const float *table, int d, int vocab, float *out,
+                        int *bad_token_flag, hipStream_t stream);
+// out = LayerNorm(x) * gamma + beta, rows of width d (eps 1e-5); optional
+// row gather (`rows`), optional multiply by `gate` after the affine.
+hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, const float *beta,
+                            const float *gate, float *out, hipStream_t stream);
+// Token shift: six outputs out[c][m, :] = x[m] + (x[m] - x_prev(m)) * mix[c],
+// x_prev(m) = x[m - 1] inside a row of T tokens, prev_state[slot[b]] at t = 0.
+hipError_t launch_token_shift(const float *x, int Bn, int T, int d, const float *prev_state,
+                              const int *slot, const float *mix6, float *out6, size_t out_stride,
+                              hipStream_t stream);
+// prev_state[slot[b]] = x[b, T - 1, :]
+hipError_t launch_save_prev(const float *x, int Bn, int T, int d, float *prev_state, const int *slot,
+                            hipStream_t stream);
+// Gather the last token of each row: out[b] = x[b, T - 1].
+hipError_t launch_gather_last(const float *x, int Bn, int T, int d, float *out, hipStream_t stream);
+// state blob pack/unpack and clearing.
+hipError_t launch_fill(float *p, size_t n, float value, hipStream_t stream);
+
+// -------------------------------------------------------------------- sampling
+hipError_t launch_sample(int n, int V, const float *logits, float temperature, int top_k,
+                         uint64_t seed, uint64_t counter, int32_t *tokens, hipStream_t stream);
+
+}  // namespace yuf

@@ -1,0 +1,156 @@
+// Device-side top-k sampling for many decode streams at once (gfx950).
+//
+// The reference samples on the host after copying every stream's logits back
+// (cli/generate.py:45-56; vulkan/src/sampler.rs:131-256).  Here one workgroup
+// per stream: temperature <= 0 takes the first maximum (torch.argmax); else the
+// top_k largest logits are found with a 4-pass 8-bit radix select over
+// order-preserving integer keys (histograms in LDS), and a Gumbel-max draw
+// argmax(x_i / T - log(-log u_i)) picks among them -- the same distribution as
+// softmax(top-k(x / T)) sampling.  u_i comes from a counter-based hash of
+// (seed, counter, stream, token id), so results do not depend on launch order.
+#include "common.h"
+#include "kernels.h"
+
+namespace yuf {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kMaxTopK = 64;
+
+__device__ __forceinline__ uint32_t order_key(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z += 0x9e3779b97f4a7c15ull;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Uniform in (0, 1) from 24 random bits.
+__device__ __forceinline__ float uniform01(uint64_t seed, uint64_t counter, int stream, int token) {
+    const uint64_t h = mix64(seed ^ mix64(counter * 0x100000001b3ull + (uint64_t)stream * 0x9e3779b97f4a7c15ull +
+                                          (uint64_t)token));
+    return ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+__global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *logits, float temperature, int top_k,
+                                                         uint64_t seed, uint64_t counter, int32_t *tokens) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t sh_prefix, sh_remaining, sh_gt, sh_eq;
+    __shared__ float cand_val[kMaxTopK];
+    __shared__ int cand_idx[kMaxTopK];
+    __shared__ float red_val[kThreads / 64];
+    __shared__ int red_idx[kThreads / 64];
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float *row = logits + (size_t)s * V;
+
+    if (!(temperature > 0.0f)) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int i = tid; i < V; i += kThreads) {
+            const float x = row[i];
+            if (x > best || (x == best && i < bi) || (isnan(x) && !isnan(best))) { best = x; bi = i; }
+        }
+        // Wave then block reduction of (value, index): larger value, then smaller index.
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(best, off);
+            const int oi = __shfl_xor(bi, off);
+            if (ov > best || (ov == best && oi < bi) || (isnan(ov) && !isnan(best))) { best = ov; bi = oi; }
+        }
+        if (lane == 0) { red_val[wave] = best; red_idx[wave] = bi; }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < kThreads / 64; ++w)
+                if (red_val[w] > best || (red_val[w] == best && red_idx[w] < bi)) { best = red_val[w]; bi = red_idx[w]; }
+            tokens[s] = bi < V ? bi : 0;
+        }
+        return;
+    }
+
+    const int k = top_k < V ? top_k : V;
+    uint32_t prefix = 0, mask = 0;
+    if (tid == 0) sh_remaining = (uint32_t)k;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        hist[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < V; i += kThreads) {
+            const uint32_t key = order_key(row[i]);
+            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t cum = 0, rem = sh_remaining;
+            int b = 255;
+            for (; b > 0; --b) {
+                if (cum + hist[b] >= rem) break;
+                cum += hist[b];
+            }
+            sh_remaining = rem - cum;
+            sh_prefix = prefix | ((uint32_t)b << shift);
+        }
+        __syncthreads();
+        prefix = sh_prefix;
+        mask |= 255u << shift;
+    }
+    // prefix = key of the k-th largest; sh_remaining = how many of its ties to keep.
+    if (tid == 0) { sh_gt = 0; sh_eq = 0; }
+    __syncthreads();
+    const uint32_t n_eq = sh_remaining;
+    const uint32_t n_gt = (uint32_t)k - n_eq;
+    for (int i = tid; i < V; i += kThreads) {
+        const float x = row[i];
+        const uint32_t key = order_key(x);
+        if (key > prefix) {
+            const uint32_t slot = atomicAdd(&sh_gt, 1u);
+            cand_val[slot] = x; cand_idx[slot] = i;
+        } else if (key == prefix) {
+            const uint32_t slot = atomicAdd(&sh_eq, 1u);
+            if (slot < n_eq) { cand_val[n_gt + slot] = x; cand_idx[n_gt + slot] = i; }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float best = -INFINITY;
+        int bi = 0x7fffffff;
+        if (lane < k) {
+            const float u = uniform01(seed, counter, s, cand_idx[lane]);
+            best = cand_val[lane] / temperature - __logf(-__logf(u));
+            bi = cand_idx[lane];
+        }
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(best, off);
+            const int oi = __shfl_xor(bi, off);
+            if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+        }
+        if (lane == 0) tokens[s] = bi < V ? bi : 0;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_sample(int n, int V, const float *logits, float temperature, int top_k, uint64_t seed,
+                         uint64_t counter, int32_t *tokens, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    if (temperature > 0.0f && (top_k < 1 || top_k > kMaxTopK)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sample_kernel, dim3(n), dim3(kThreads), 0, stream, V, logits, temperature, top_k, seed,
+                       counter, tokens);
+    return hipGetLastError();
+}
+
+}  // namespace yuf
+
+extern "C" int yuf_sample_device(int n, int V, const float *logits_dev, float temperature, int top_k, uint64_t seed,
+                                 uint64_t counter, int32_t *tokens_dev, void *stream) {
+    using namespace yuf;
+    if (n < 0 || V <= 0) return fail(YUF_ERR_INVALID, "sample_device: bad sizes");
+    if (temperature > 0.0f && (top_k < 1 || top_k > kMaxTopK))
+        return fail(YUF_ERR_INVALID, "sample_device: top_k must be in [1, 64] when temperature > 0");
+    if (n > 0 && (!logits_dev || !tokens_dev)) return fail(YUF_ERR_INVALID, "sample_device: null pointer");
+    hipError_t err = launch_sample(n, V, logits_dev, temperature, top_k, seed, counter, tokens_dev,
+                                   static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("sample launch: ") + hipGetErrorString(err));
+    return YUF_OK;
+}

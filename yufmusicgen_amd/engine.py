@@ -1,0 +1,219 @@
+"""Python host mirror of the engine API (the C ABI of ``include/yuf_engine.h``).
+
+Keeps the reference engine's surface -- ``Checkpoint.load`` /
+``Model(ckpt)`` / ``model.step(token)`` / ``model.reset_state()`` and the
+sampler's ``Mt19937`` / ``sample_token`` / ``argmax`` (vulkan/src/checkpoint.rs,
+vulkan/src/compute/model.rs:24-65, vulkan/src/sampler.rs) -- and adds the
+batched multi-stream calls (prefill, step, state save/load) the HIP engine
+provides.  Host arrays are numpy; the ``*_device`` calls take torch GPU
+tensors (torch is only the device-memory plumbing).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+from ._lib import ModelConfigC, RngC, c_float_p, check, lib
+
+LOGITS_NONE, LOGITS_LAST, LOGITS_ALL = 0, 1, 2
+_MODES = {"none": LOGITS_NONE, "last": LOGITS_LAST, "all": LOGITS_ALL}
+
+
+def _config_dict(c: ModelConfigC) -> dict:
+    return {name: getattr(c, name) for name, _ in ModelConfigC._fields_}
+
+
+class Checkpoint:
+    """A loaded ``.yuf`` file (``Checkpoint::load``, checkpoint.rs:90-149)."""
+
+    def __init__(self, handle):
+        self._h = handle
+
+    @classmethod
+    def load(cls, path) -> "Checkpoint":
+        handle = ctypes.c_void_p()
+        check(lib().yuf_ckpt_load(str(Path(path)).encode(), ctypes.byref(handle)))
+        return cls(handle)
+
+    @property
+    def config(self) -> dict:
+        c = ModelConfigC()
+        check(lib().yuf_ckpt_config(self._h, ctypes.byref(c)))
+        return _config_dict(c)
+
+    def tensor(self, name: str) -> np.ndarray:
+        """``Checkpoint::tensor`` + ``tensor_dims`` (checkpoint.rs:151-168); a copy."""
+        data = c_float_p()
+        count = ctypes.c_int64()
+        ndim = ctypes.c_int32()
+        dims = (ctypes.c_int64 * 8)()
+        check(lib().yuf_ckpt_tensor(self._h, name.encode(), ctypes.byref(data), ctypes.byref(count),
+                                    ctypes.byref(ndim), dims))
+        flat = np.ctypeslib.as_array(data, shape=(count.value,)).copy()
+        return flat.reshape([dims[i] for i in range(ndim.value)])
+
+    def close(self) -> None:
+        if self._h:
+            lib().yuf_ckpt_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Engine:
+    """Device-resident weights and ``max_streams`` recurrent-state slots."""
+
+    def __init__(self, ckpt: Checkpoint, max_streams: int = 1, max_tokens: int = 4096):
+        handle = ctypes.c_void_p()
+        check(lib().yuf_engine_create(ckpt._h, int(max_streams), int(max_tokens), ctypes.byref(handle)))
+        self._h = handle
+        c = ModelConfigC()
+        check(lib().yuf_engine_config(self._h, ctypes.byref(c)))
+        self.config = _config_dict(c)
+        self.vocab = self.config["vocab_size"]
+        self.max_streams = int(max_streams)
+
+    # ---------------------------------------------------------------- host API
+    @staticmethod
+    def _slots(n, slots):
+        arr = np.arange(n, dtype=np.int32) if slots is None else np.ascontiguousarray(slots, dtype=np.int32)
+        if arr.shape != (n,):
+            raise ValueError("slots must have one entry per stream")
+        return arr
+
+    def prefill(self, tokens, slots=None, logits: str = "last"):
+        """Run ``tokens`` [n, T] through the model from each slot's current state.
+
+        Returns logits ``[n, V]`` ("last"), ``[n, T, V]`` ("all") or None ("none")."""
+        tok = np.ascontiguousarray(tokens, dtype=np.int32)
+        if tok.ndim != 2:
+            raise ValueError("tokens must have shape [n, T]")
+        n, steps = tok.shape
+        mode = _MODES[logits]
+        sl = self._slots(n, slots)
+        out = None
+        if mode == LOGITS_LAST:
+            out = np.empty((n, self.vocab), np.float32)
+        elif mode == LOGITS_ALL:
+            out = np.empty((n, steps, self.vocab), np.float32)
+        check(lib().yuf_prefill(self._h, n, sl.ctypes.data, steps, tok.ctypes.data,
+                                None if out is None else out.ctypes.data, mode))
+        return out
+
+    def step(self, tokens, slots=None) -> np.ndarray:
+        """One token per stream -> logits [n, V] (``Model::step``, model.rs:54-60)."""
+        tok = np.ascontiguousarray(np.atleast_1d(tokens), dtype=np.int32)
+        n = tok.shape[0]
+        out = np.empty((n, self.vocab), np.float32)
+        check(lib().yuf_step(self._h, n, self._slots(n, slots).ctypes.data, tok.ctypes.data, out.ctypes.data))
+        return out
+
+    def reset_state(self, slot: int = -1) -> None:
+        check(lib().yuf_state_reset(self._h, int(slot)))
+
+    @property
+    def state_size(self) -> int:
+        return int(lib().yuf_state_size(self._h))
+
+    def save_state(self, slot: int) -> np.ndarray:
+        blob = np.empty(self.state_size // 4, np.float32)
+        check(lib().yuf_state_save(self._h, int(slot), blob.ctypes.data))
+        return blob
+
+    def load_state(self, slot: int, blob) -> None:
+        arr = np.ascontiguousarray(blob, dtype=np.float32)
+        if arr.size * 4 != self.state_size:
+            raise ValueError(f"state blob must hold {self.state_size // 4} floats")
+        check(lib().yuf_state_load(self._h, int(slot), arr.ctypes.data))
+
+    # -------------------------------------------------------------- device API
+    @property
+    def stream(self) -> int:
+        return int(lib().yuf_engine_stream(self._h) or 0)
+
+    def prefill_device(self, tokens_dev, logits_dev, slots, logits: str = "last") -> None:
+        """Asynchronous on the engine's stream; tokens [n, T] int32, logits float32 GPU tensors."""
+        n, steps = tokens_dev.shape
+        sl = self._slots(n, slots)
+        check(lib().yuf_prefill_device(self._h, n, sl.ctypes.data, steps, tokens_dev.data_ptr(),
+                                       None if logits_dev is None else logits_dev.data_ptr(), _MODES[logits]))
+
+    def step_device(self, tokens_dev, logits_dev, slots) -> None:
+        n = tokens_dev.shape[0]
+        check(lib().yuf_step_device(self._h, n, self._slots(n, slots).ctypes.data, tokens_dev.data_ptr(),
+                                    logits_dev.data_ptr()))
+
+    def close(self) -> None:
+        if self._h:
+            lib().yuf_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Model:
+    """Single-stream drop-in for the reference ``Model`` (model.rs:24-65)."""
+
+    def __init__(self, ckpt: Checkpoint):
+        self.engine = Engine(ckpt, max_streams=1, max_tokens=4096)
+        self.config = self.engine.config
+
+    def step(self, token: int) -> np.ndarray:
+        return self.engine.step([int(token)])[0]
+
+    def reset_state(self) -> None:
+        self.engine.reset_state(0)
+
+
+# ------------------------------------------------------------------- sampling
+class Mt19937:
+    """torch's CPU generator (``torch.manual_seed``), sampler.rs:22-82."""
+
+    def __init__(self, seed: int):
+        self._rng = RngC()
+        lib().yuf_rng_seed(ctypes.byref(self._rng), int(seed) & 0xFFFFFFFFFFFFFFFF)
+
+    def next_u32(self) -> int:
+        return int(lib().yuf_rng_next_u32(ctypes.byref(self._rng)))
+
+    def next_uniform(self) -> float:
+        return float(lib().yuf_rng_next_uniform(ctypes.byref(self._rng)))
+
+
+def sample_token(logits, temperature: float, top_p: float, rng: Mt19937, top_k: int = 0) -> int:
+    """Token-for-token torch's CPU ``sample_token`` (cli/generate.py:45-56) under the same seed."""
+    arr = np.ascontiguousarray(logits, dtype=np.float32)
+    out = lib().yuf_sample(arr.ctypes.data, arr.size, float(temperature), float(top_p), int(top_k),
+                           ctypes.byref(rng._rng))
+    if out < 0:
+        check(out)
+    return int(out)
+
+
+def argmax(logits) -> int:
+    arr = np.ascontiguousarray(logits, dtype=np.float32)
+    out = lib().yuf_argmax(arr.ctypes.data, arr.size)
+    if out < 0:
+        check(out)
+    return int(out)
+
+
+def sample_device(logits_dev, tokens_dev, temperature: float, top_k: int, seed: int, counter: int, stream=None):
+    """Top-k sampling of every row of ``logits_dev`` [n, V] on the GPU."""
+    n, vocab = logits_dev.shape
+    import torch
+
+    st = torch.cuda.current_stream().cuda_stream if stream is None else stream
+    check(lib().yuf_sample_device(n, vocab, logits_dev.data_ptr(), float(temperature), int(top_k), int(seed),
+                                  int(counter), tokens_dev.data_ptr(), st))
