@@ -1,0 +1,257 @@
+"""Benchmark of the YufMusicGen recurrent hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+One "step" is the C3 prefill of BASELINE.json: the default 0.1B model
+(14 layers, d_model 640, 16 heads x 40, ROSA 128, vocab 20 480, random fp32
+weights from a seed) over B = 8 rows x T = 2048 synthetic token ids, every
+position's logits written to HBM.  Token ids and weights are resident in HBM
+before the timed region; W untimed steps, then exactly K timed steps between
+device synchronisations.  `value` = B*T*K / elapsed (prefill tokens/s).
+
+In the same run:
+  * decode (C4): 64 streams prefilled with 256 tokens, then 1024 single-token
+    steps with on-device temperature-1.0 top-k=32 sampling -> decode tokens/s;
+  * the WKV-7 scan (C2: B=8, T=2048, H=16, N=40, zero state) timed with HIP
+    events on the stream it runs on -> `roofline` (algorithmic bytes / time
+    against the 8 TB/s HBM peak);
+  * the FFN in/gate projection GEMM of C3 (M=16384, N=5120, K=640) -> MFMA
+    utilisation against the 157.3 TFLOP/s dense fp32 peak;
+  * `cpu_baseline`: the oracle's float32 restatement of the reference's PyTorch
+    CPU fallback on a bounded slice of C3 (same model, B=8 x T=1024), timed on
+    this host's cores (~10-30 s of CPU work).
+
+Only N = 1 GPU exists on these boxes; --gpus above 1 exits with a message.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "prefill+decode tokens/s, 0.1B model B=8 T=2048; WKV-7 scan % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def wkv_bytes(B, T, H, N, nonzero_state=False) -> int:
+    """Algorithmic HBM bytes of one scan: r, w, k, v, a, b in, y out, final state out (+ state in)."""
+    return 4 * (7 * B * T * H * N + B * H * N * N * (2 if nonzero_state else 1))
+
+
+def time_events(fn, iters: int, stream=None) -> float:
+    """Average ms per call, HIP events recorded on `stream` (a torch.cuda.Stream)."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def bench_scan(iters: int) -> dict:
+    import torch
+
+    from yufmusicgen_amd.ops import rwkv7_scan
+    from yufmusicgen_amd.synth import wkv_inputs
+
+    B, T, H, N = 8, 2048, 16, 40
+    dev = [torch.from_numpy(x).cuda() for x in wkv_inputs(0, B, T, H, N)]
+    rwkv7_scan(*dev)
+    torch.cuda.synchronize()
+    ms = time_events(lambda: rwkv7_scan(*dev), iters, torch.cuda.current_stream())
+    nbytes = wkv_bytes(B, T, H, N)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    traffic = None
+    pmc = os.path.join(ROOT, "profiles", "wkv7_scan_c2_traffic.json")
+    if os.path.exists(pmc):
+        with open(pmc) as handle:
+            traffic = json.load(handle).get("traffic_bytes")
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": "wkv7_scan_kernel<40,false> (C2: B=8 T=2048 H=16 N=40)",
+            "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
+
+
+def bench_gemm(iters: int) -> dict:
+    import torch
+
+    from yufmusicgen_amd._lib import check, lib
+
+    M, N, K = 16384, 5120, 640
+    a = torch.randn(M, K, device="cuda")
+    w = torch.randn(N, K, device="cuda") * 0.02
+    c = torch.empty(M, N, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    run = lambda: check(lib().yuf_linear_f32(M, N, K, a.data_ptr(), w.data_ptr(), None, 0, None,  # noqa: E731
+                                             c.data_ptr(), st))
+    run()
+    torch.cuda.synchronize()
+    ms = time_events(run, iters, torch.cuda.current_stream())
+    tflops = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tflops / FP32_MFMA_PEAK_TFLOPS, 4), "kernel": "gemm_f32_kernel M=16384 N=5120 K=640",
+            "avg_us": round(ms * 1e3, 1)}
+
+
+def cpu_baseline(weights, cfg) -> dict:
+    import torch
+
+    from oracle.model import OracleModel
+    from yufmusicgen_amd.synth import prompt_tokens
+
+    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
+    cores = torch.get_num_threads()
+    B, T = 8, 1024
+    tokens = prompt_tokens(7, B, T, cfg.vocab_size)
+    model = OracleModel(cfg.to_dict(), weights, dtype=torch.float32)
+    with torch.no_grad():
+        model.forward(tokens[:, :4])  # warm-up
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            model.forward(tokens, logits="all")
+            times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    return {"value": round(B * T / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"C3 prefill slice B={B} x T={T} (0.1B model, all-position logits), fp32 torch CPU "
+                      f"restatement of the reference fallback, median of 3 = {sec:.2f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--decode-steps", type=int, default=1024)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path shards data-parallel over streams, see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from yufmusicgen_amd.checkpoint import write_yuf
+    from yufmusicgen_amd.config import PRESETS
+    from yufmusicgen_amd.engine import Checkpoint, Engine, sample_device
+    from yufmusicgen_amd.synth import prompt_tokens, synth_weights, uniform_tokens
+
+    cfg = PRESETS["0.1b"]
+    log("generating weights")
+    weights = synth_weights(cfg, seed=0)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "model.yuf")
+        write_yuf(path, cfg, weights)
+        ckpt = Checkpoint.load(path)
+    B, T = 8, 2048
+    engine = Engine(ckpt, max_streams=64, max_tokens=B * T)
+    stream = torch.cuda.ExternalStream(engine.stream)
+    tokens = torch.from_numpy(prompt_tokens(0, B, T, cfg.vocab_size)).cuda()
+    logits = torch.empty(B, T, cfg.vocab_size, device="cuda")
+    slots = np.arange(B, dtype=np.int32)
+
+    def prefill_step():
+        engine.prefill_device(tokens, logits, slots, logits="all")
+
+    log("prefill warmup")
+    for _ in range(args.warmup):
+        engine.reset_state()
+        prefill_step()
+    torch.cuda.synchronize()
+    log("prefill timed")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        prefill_step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    prefill_tps = B * T * args.steps / elapsed
+    log(f"prefill {ms_per_step:.2f} ms/step, {prefill_tps:.0f} tokens/s")
+
+    # C4 decode: 64 streams x 256-token prefill, then decode with device top-k sampling.
+    S, P = 64, 256
+    engine.reset_state()
+    dec_tokens = torch.from_numpy(uniform_tokens(3, S, P, cfg.vocab_size)).cuda()
+    last_logits = torch.empty(S, cfg.vocab_size, device="cuda")
+    dslots = np.arange(S, dtype=np.int32)
+    engine.prefill_device(dec_tokens, last_logits, dslots, logits="last")
+    step_tok = torch.empty(S, dtype=torch.int32, device="cuda")
+    with torch.cuda.stream(stream):
+        sample_device(last_logits, step_tok, 1.0, 32, seed=1234, counter=0, stream=engine.stream)
+    for i in range(3):  # warm-up steps
+        engine.step_device(step_tok, last_logits, dslots)
+        sample_device(last_logits, step_tok, 1.0, 32, seed=1234, counter=i + 1, stream=engine.stream)
+    torch.cuda.synchronize()
+    log("decode timed")
+    t0 = time.perf_counter()
+    for i in range(args.decode_steps):
+        engine.step_device(step_tok, last_logits, dslots)
+        sample_device(last_logits, step_tok, 1.0, 32, seed=1234, counter=100 + i, stream=engine.stream)
+    torch.cuda.synchronize()
+    dec_elapsed = time.perf_counter() - t0
+    decode_tps = S * args.decode_steps / dec_elapsed
+    log(f"decode {dec_elapsed * 1e3 / args.decode_steps:.3f} ms/step, {decode_tps:.0f} tokens/s")
+    engine.close()
+    del logits
+
+    log("scan roofline")
+    roofline = bench_scan(20)
+    log(f"scan {roofline['avg_us']} us, {roofline['achieved']} GB/s")
+    gemm = bench_gemm(10)
+    log(f"gemm {gemm['achieved']} TFLOP/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(weights, cfg)
+        log(f"cpu {cpu['value']} tokens/s on {cpu['cores']} cores")
+
+    out = {
+        "metric": METRIC,
+        "value": round(prefill_tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "C3 prefill: 0.1B model (14L, d640, 16x40 heads, ROSA 128, V 20480, seeded fp32 weights), "
+                        "B=8 x T=2048 token ids, all-position logits",
+            "decode_workload": f"C4: 64 streams prefilled with 256 tokens, {args.decode_steps} steps, "
+                               "device top-k=32 T=1.0 sampling",
+        },
+        "decode_tokens_per_s": round(decode_tps, 1),
+        "decode_ms_per_step": round(dec_elapsed * 1e3 / args.decode_steps, 3),
+        "roofline": roofline,
+        "gemm_roofline": gemm,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
