@@ -64,6 +64,8 @@ struct Engine {
     float *h = nullptr, *xn = nullptr, *mix = nullptr, *r = nullptr, *k = nullptr, *v = nullptr, *wr = nullptr,
           *al = nullptr, *g = nullptr, *lr = nullptr, *y = nullptr, *z = nullptr, *rosa3 = nullptr, *rread = nullptr,
           *ffn = nullptr, *hl = nullptr;
+    float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
+    size_t gemm_ws_floats = 0;
     int *slots_dev = nullptr, *tokens_dev = nullptr, *bad_dev = nullptr;
     int *slots_host = nullptr;  // pinned
     std::vector<int> last_slots;
@@ -221,6 +223,7 @@ int gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W
     GemmParams p;
     p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.C = C; p.ldc = ldc;
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = ldr; p.silu_pair = silu_pair;
+    p.workspace = e.gemm_ws; p.workspace_floats = e.gemm_ws_floats;
     ENG_TRY(launch_gemm(p, e.stream), "gemm");
     return YUF_OK;
 }
@@ -418,16 +421,24 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
 
     // Workspace.
     const size_t Mx = (size_t)max_tokens, d = s.d;
+    size_t ws = 0;
+    {
+        const int D = s.rosa, L = s.low_rank, dd = s.d;
+        const int shapes[][2] = {{dd, dd}, {L, dd}, {dd, L}, {3 * D, dd}, {dd, D}, {8 * dd, dd}, {dd, 4 * dd},
+                                 {s.vocab, dd}};
+        for (auto &nk : shapes) ws = std::max(ws, gemm_workspace_floats(nk[0], nk[1]));
+    }
+    e.gemm_ws_floats = ws;
     const size_t sizes[] = {Mx * d, Mx * d, 6 * Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d,
                             Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
-                            (size_t)max_streams * d};
+                            (size_t)max_streams * d, ws};
     size_t total = 0;
     for (size_t z : sizes) total += ((z * sizeof(float) + 255) / 256) * 256;
     ENG_TRY(hipMalloc(&e.work.p, total), "workspace alloc");
     {
         char *cur = static_cast<char *>(e.work.p);
         float **dst[] = {&e.h, &e.xn, &e.mix, &e.r, &e.k, &e.v, &e.wr, &e.al, &e.g, &e.lr, &e.y, &e.z, &e.rosa3,
-                         &e.rread, &e.ffn, &e.hl};
+                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws};
         for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
     }
     const size_t io_bytes = 256 * 3 + (size_t)(max_streams + max_tokens + 1) * sizeof(int);

@@ -19,6 +19,8 @@
 // Epilogues fused into the store: + bias[n], tanh / sigmoid, + residual, and
 // the paired SiLU gate of the FFN (W rows interleaved in blocks of 32 "in"
 // then 32 "gate" rows; output silu(in) * gate).
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -180,6 +182,170 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmParams p, int ti
     }
 }
 
+// ---------------------------------------------------------------------------
+// Short-M path (decode: M <= 64 rows, one token per stream).  The product is
+// bound by streaming W from HBM, so parallelism comes from N and K instead of
+// M: each wave owns 64 rows x 64 columns (2 x 2 MFMA 32x32 tiles) over a K
+// slice, reading A (small, L2-resident) and W directly from global memory with
+// 16-float contiguous runs per lane; split-K partials go to a workspace and a
+// second kernel sums them in a fixed order and applies the epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kSkinnyWaves = 4;
+constexpr int kSkinnyTargetWaves = 1024;
+
+struct SkinnyFrag {
+    float v[16];
+};
+
+__device__ __forceinline__ void skinny_load(SkinnyFrag &f, __amdgpu_buffer_rsrc_t rsrc, int row, int ld, int k,
+                                            int K) {
+    if (k + 15 < K) {
+        const uint32_t off = (uint32_t)((size_t)row * ld + k) * 4u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const auto raw = __builtin_amdgcn_raw_buffer_load_b128(rsrc, off + q * 16, 0, 0);
+            const float4 x = __builtin_bit_cast(float4, raw);
+            f.v[4 * q] = x.x; f.v[4 * q + 1] = x.y; f.v[4 * q + 2] = x.z; f.v[4 * q + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 16; ++q)
+            f.v[q] = buf_load(rsrc, k + q < K ? (uint32_t)((size_t)row * ld + k + q) * 4u : kBufferOob);
+    }
+}
+
+__device__ __forceinline__ void store_out(const GemmParams &p, int row, int col, float x) {
+    x = apply_act(x + (p.bias ? p.bias[col] : 0.0f), p.act);
+    if (p.residual) x += p.residual[(size_t)row * p.ldr + col];
+    p.C[(size_t)row * p.ldc + col] = x;
+}
+
+__global__ void __launch_bounds__(64 * kSkinnyWaves) gemm_skinny_kernel(GemmParams p, int k_chunk, int splits) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * kSkinnyWaves + wave) * 64;
+    if (n0 >= p.N) return;
+    const int split = blockIdx.y;
+    const int k_begin = split * k_chunk;
+    const int k_end = min(p.K, k_begin + k_chunk);
+    const int rows = min(p.M, 64);
+    const auto ra = make_rsrc(p.A, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
+    const int ncols = min(64, p.N - n0);
+    const auto rw = make_rsrc(p.W + (size_t)n0 * p.ldw, (uint32_t)(((size_t)(ncols - 1) * p.ldw + p.K) * 4));
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx16{};
+    const int r_in = lane & 31, k_half = (lane >> 5) * 16;
+    SkinnyFrag a[2], w[2], an[2], wn[2];
+    int k = k_begin;
+    if (k < k_end) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            skinny_load(a[i], ra, i * 32 + r_in, p.lda, k + k_half, k_end);
+            skinny_load(w[i], rw, i * 32 + r_in, p.ldw, k + k_half, k_end);
+        }
+    }
+    for (; k < k_end; k += 32) {
+        const bool more = k + 32 < k_end;
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                skinny_load(an[i], ra, i * 32 + r_in, p.lda, k + 32 + k_half, k_end);
+                skinny_load(wn[i], rw, i * 32 + r_in, p.ldw, k + 32 + k_half, k_end);
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i].v[s], w[j].v[s], acc[i][j], 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) { a[i] = an[i]; w[i] = wn[i]; }
+        }
+    }
+    const int col_in_tile = lane & 31, row_base = (lane >> 5) * 4;
+    if (splits > 1) {
+        float *part = p.workspace + (size_t)split * p.M * p.N;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + j * 32 + col_in_tile;
+            if (col >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = i * 32 + (r >> 2) * 8 + row_base + (r & 3);
+                    if (row < p.M) part[(size_t)row * p.N + col] = acc[i][j][r];
+                }
+        }
+        return;
+    }
+    if (p.silu_pair) {
+        const int hcol = n0 / 2 + col_in_tile;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = i * 32 + (r >> 2) * 8 + row_base + (r & 3);
+                if (row < p.M) {
+                    const float x = acc[i][0][r], g = acc[i][1][r];
+                    p.C[(size_t)row * p.ldc + hcol] = x / (1.0f + expf(-x)) * g;
+                }
+            }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int col = n0 + j * 32 + col_in_tile;
+        if (col >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = i * 32 + (r >> 2) * 8 + row_base + (r & 3);
+                if (row < p.M) store_out(p, row, col, acc[i][j][r]);
+            }
+    }
+}
+
+// Sum the split-K partials in split order and apply the epilogue.
+__global__ void gemm_splitk_reduce_kernel(GemmParams p, int splits) {
+    const int out_cols = p.silu_pair ? p.N / 2 : p.N;
+    const size_t total = (size_t)p.M * out_cols;
+    const size_t plane = (size_t)p.M * p.N;
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * blockDim.x) {
+        const int row = (int)(idx / out_cols), c = (int)(idx - (size_t)row * out_cols);
+        if (p.silu_pair) {
+            const int q = c / 32, cc = c - q * 32;
+            const int cin = q * 64 + cc, cgate = cin + 32;
+            float x = 0.0f, g = 0.0f;
+            for (int s = 0; s < splits; ++s) {
+                x += p.workspace[s * plane + (size_t)row * p.N + cin];
+                g += p.workspace[s * plane + (size_t)row * p.N + cgate];
+            }
+            p.C[(size_t)row * p.ldc + c] = x / (1.0f + expf(-x)) * g;
+        } else {
+            float x = 0.0f;
+            for (int s = 0; s < splits; ++s) x += p.workspace[s * plane + (size_t)row * p.N + c];
+            store_out(p, row, c, x);
+        }
+    }
+}
+
+int skinny_splits(int N, int K) {
+    const int wave_tiles = (N + 63) / 64;
+    const int max_splits = (K + 31) / 32;
+    int s = (kSkinnyTargetWaves + wave_tiles - 1) / wave_tiles;
+    s = s < 1 ? 1 : (s > max_splits ? max_splits : s);
+    return s > 64 ? 64 : s;
+}
+
 }  // namespace
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
@@ -188,6 +354,21 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
     // Buffer descriptors address at most 2^31 bytes per 128-row panel.
     if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
+    if (p.M <= 64) {
+        int splits = skinny_splits(p.N, p.K);
+        if (!p.workspace || (size_t)splits * p.M * p.N > p.workspace_floats) splits = 1;
+        const int k_chunk = ((p.K + splits - 1) / splits + 31) / 32 * 32;
+        splits = (p.K + k_chunk - 1) / k_chunk;
+        const int wave_tiles = (p.N + 63) / 64;
+        const dim3 grid((wave_tiles + kSkinnyWaves - 1) / kSkinnyWaves, splits);
+        hipLaunchKernelGGL(gemm_skinny_kernel, grid, dim3(64 * kSkinnyWaves), 0, stream, p, k_chunk, splits);
+        if (splits > 1) {
+            const size_t outs = (size_t)p.M * (p.silu_pair ? p.N / 2 : p.N);
+            const int blocks = (int)std::min<size_t>((outs + 255) / 256, 4096);
+            hipLaunchKernelGGL(gemm_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, stream, p, splits);
+        }
+        return hipGetLastError();
+    }
     const int tiles_m = (p.M + kBM - 1) / kBM, tiles_n = (p.N + kBN - 1) / kBN;
     const int total = tiles_m * tiles_n;
     const int per_xcd = (total + kXcds - 1) / kXcds;
@@ -195,6 +376,8 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
                        per_xcd);
     return hipGetLastError();
 }
+
+size_t gemm_workspace_floats(int N, int K) { return (size_t)skinny_splits(N, K) * 64 * N; }
 
 }  // namespace yuf
 

@@ -60,8 +60,14 @@ struct GemmParams {
     // Paired SiLU-gate output: W rows come in blocks of 64 = 32 "in" rows then
     // 32 "gate" rows; C[m, 32 q + c] = silu(in) * gate.  N counts W rows.
     bool silu_pair = false;
+    // Optional scratch for the split-K path of short-M (decode) products:
+    // `workspace_floats` floats of device memory; nullptr disables splitting.
+    float *workspace = nullptr;
+    size_t workspace_floats = 0;
 };
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
+// Workspace the short-M path can use for an N-column product (floats).
+size_t gemm_workspace_floats(int N, int K);
 
 // ---------------------------------------------------------------- elementwise
 hipError_t launch_embed(const int *tokens, int M, const float *table, int d, int vocab, float *out,
