@@ -74,6 +74,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also releases
+// global memory at workgroup scope, which makes every wave wait for its
+// outstanding global loads -- including prefetches meant to stay in flight
+// across the barrier.  The kernels here exchange data through LDS only.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------------------------
 // Raw buffer loads: the hardware bounds-checks every access against the
 // descriptor's byte range and returns 0 outside it, so staging loops need no
@@ -89,6 +99,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
 __device__ __forceinline__ float buf_load(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsrc, byte_offset, 0, 0));
 }
+
+__device__ __forceinline__ void buf_store(float value, __amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, value), rsrc, byte_offset, 0, 0);
+}
+
+// s_waitcnt vmcnt(0): retire this wave's outstanding global loads here, so the
+// compiler's conservative wait insertion does not place a full wait inside a
+// later loop (where it would also wait for prefetches issued in that loop).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 

@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmParams p, int ti
     load_tile(tb, w_base, p.ldw, p.N - n0, 0, p.K, tid);
     store_tile(ta, As[0], tid);
     store_tile(tb, Bs[0], tid);
-    __syncthreads();
+    lds_barrier();
 
     const int frag_row = lane & 31, frag_k = (lane >> 5) * 16;
     for (int kt = 0; kt < k_tiles; ++kt) {
@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmParams p, int ti
             store_tile(ta, As[cur ^ 1], tid);
             store_tile(tb, Bs[cur ^ 1], tid);
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // Epilogue.  Accumulator element r of lane l holds

@@ -52,116 +52,143 @@ template <int N>
 struct Layout {
     static constexpr int L = Shape<N>::L;
     static constexpr int E = Shape<N>::E;
-    static constexpr int R = kWave / L;                  // rows per wave
-    static constexpr int W = (N + R - 1) / R;            // waves per head
-    static constexpr int P = ((5 * E + 3) / 4) * 4;      // floats per (token, lane-column)
-    static constexpr int kCols = kChunk * L * P;         // one LDS buffer of column vectors
-    static constexpr int kItems = (kChunk * N + kWave - 1) / kWave;  // staging items per lane
-    static constexpr int kVItems = (kChunk * R + kWave - 1) / kWave;
+    static constexpr int R = kWave / L;                        // rows per wave
+    static constexpr int W = (N + R - 1) / R;                  // waves per head
+    static constexpr int P = ((5 * E + 3) / 4) * 4;            // floats per (token, lane-column)
+    static constexpr int kCols = kChunk * L * P;               // staged operands of one chunk
+    static constexpr int kF4 = N / 4;                          // float4 per token row of a head
+    static constexpr int kItems = (kChunk * kF4 + kWave - 1) / kWave;
+    static constexpr int kVF4 = R / 4;                         // float4 of v per token
+    static constexpr int kVItems = (kChunk * kVF4 + kWave - 1) / kWave;
 };
 
-// Vector slots inside a lane's P floats: [a | d | b | k | r], E each.
+// Operand slots inside a lane's P floats: [a | d | b | k | r], E each.
 enum : int { kA = 0, kD = 1, kB = 2, kK = 3, kR = 4 };
+// Raw per-token vectors staged before the decay pass.
+enum : int { kRawR = 0, kRawW = 1, kRawK = 2, kRawA = 3, kRawB = 4, kNumRaw = 5 };
 
-template <int N, bool PREP>
+template <int N>
 struct Stage {
     using Lay = Layout<N>;
-    float r[Lay::kItems], w[Lay::kItems], k[Lay::kItems], a[Lay::kItems], b[Lay::kItems];
-    float v[Lay::kVItems];
+    float4 x[kNumRaw][Lay::kItems];
+    float4 v[Lay::kVItems];
 };
 
-template <int N, bool PREP>
-__device__ __forceinline__ void stage_load(Stage<N, PREP> &st, const WkvParams &p, int bb, int h,
-                                           int row0, int t0, int nt, int lane) {
-    using Lay = Layout<N>;
-    // Token t of this chunk starts t * H * N floats after `base`; tokens past
-    // the chunk end fall outside the descriptor range and load as 0.
-    const size_t base = ((size_t)(bb * p.T + t0) * p.H + h) * N;
-    const uint32_t bytes = nt > 0 ? (uint32_t)(((nt - 1) * p.H * N + N) * 4) : 0u;
-    const auto rr_ = make_rsrc(p.r + base, bytes), rw_ = make_rsrc(p.w + base, bytes);
-    const auto rk_ = make_rsrc(p.k + base, bytes), ra_ = make_rsrc(p.a + base, bytes);
-    const auto rv_ = make_rsrc(p.v + base, bytes);
-    const int stride = p.H * N;
-#pragma unroll
-    for (int it = 0; it < Lay::kItems; ++it) {
-        const int q = lane + it * kWave;
-        const int t = q / N, j = q - t * N;
-        const uint32_t off = (uint32_t)(t * stride + j) * 4u;
-        st.r[it] = buf_load(rr_, off);
-        st.w[it] = buf_load(rw_, off);
-        st.k[it] = buf_load(rk_, off);
-        st.a[it] = buf_load(ra_, off);
-        if constexpr (!PREP) st.b[it] = buf_load(make_rsrc(p.b + base, bytes), off);
-    }
-#pragma unroll
-    for (int it = 0; it < Lay::kVItems; ++it) {
-        const int q = lane + it * kWave;
-        const int t = q / Lay::R, rr = q - t * Lay::R;
-        const bool ok = row0 + rr < N && q < kChunk * Lay::R;
-        st.v[it] = buf_load(rv_, ok ? (uint32_t)(t * stride + row0 + rr) * 4u : kBufferOob);
-    }
+__device__ __forceinline__ float4 buf_load4(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, 0));
 }
 
-// Transform the prefetched registers into the LDS layout of buffer `cols`.
+// Issue the HBM reads of one chunk (16-byte bounds-checked buffer loads; tokens
+// past the chunk end fall outside the descriptors and read as 0).
 template <int N, bool PREP>
-__device__ __forceinline__ void stage_store(Stage<N, PREP> &st, const WkvParams &p, int h, int nt,
-                                            int lane, float *cols, float *vbuf, float *sq, float *inv_norm) {
+__device__ __forceinline__ void stage_load(Stage<N> &st, const WkvParams &p, int bb, int h, int row0, int t0,
+                                           int nt, int lane) {
     using Lay = Layout<N>;
-    constexpr int E = Lay::E, P = Lay::P, L = Lay::L;
-    float kk[Lay::kItems];
-    if constexpr (PREP) {
-        // Per-token L2 norm of k * k_k over the head (F.normalize, eps 1e-12),
-        // summed in a fixed order so results are deterministic.
+    const size_t base = ((size_t)(bb * p.T + t0) * p.H + h) * N;
+    const uint32_t bytes = nt > 0 ? (uint32_t)(((nt - 1) * p.H * N + N) * 4) : 0u;
+    const float *src[kNumRaw] = {p.r, p.w, p.k, p.a, PREP ? p.a : p.b};
+    const int stride = p.H * N;
+#pragma unroll
+    for (int c = 0; c < (PREP ? kNumRaw - 1 : kNumRaw); ++c) {
+        const auto rs = make_rsrc(src[c] + base, bytes);
 #pragma unroll
         for (int it = 0; it < Lay::kItems; ++it) {
             const int q = lane + it * kWave;
-            const int t = q / N, j = q - t * N;
-            kk[it] = 0.0f;
-            if (q < kChunk * N && t < nt) {
-                kk[it] = st.k[it] * p.k_k[h * N + j];
-                sq[q] = kk[it] * kk[it];
+            const int t = q / Lay::kF4, f = q - t * Lay::kF4;
+            st.x[c][it] = buf_load4(rs, q < kChunk * Lay::kF4 ? (uint32_t)(t * stride + f * 4) * 4u : kBufferOob);
+        }
+    }
+    const auto rv = make_rsrc(p.v + base, bytes);
+#pragma unroll
+    for (int it = 0; it < Lay::kVItems; ++it) {
+        const int q = lane + it * kWave;
+        const int t = q / Lay::kVF4, f = q - t * Lay::kVF4;
+        const bool ok = q < kChunk * Lay::kVF4 && row0 + f * 4 < N;
+        st.v[it] = buf_load4(rv, ok ? (uint32_t)(t * stride + row0 + f * 4) * 4u : kBufferOob);
+    }
+}
+
+// Turn a staged chunk into the per-lane operand layout: for token t and lane
+// column group cl, P contiguous floats [a | d | b | k | r] (E each), so a lane
+// fetches one token's operands with ds_read_b128.  Work is spread over all
+// lanes as (token, 4-column) items.
+template <int N, bool PREP>
+__device__ __forceinline__ void stage_store(const Stage<N> &st, const WkvParams &p, int h, int nt, int lane,
+                                            float *raw, float *cols, float *vbuf, float *psq, float *inv_norm) {
+    using Lay = Layout<N>;
+    constexpr int E = Lay::E, P = Lay::P, L = Lay::L, F4 = Lay::kF4;
+#pragma unroll
+    for (int c = 0; c < (PREP ? kNumRaw - 1 : kNumRaw); ++c)
+#pragma unroll
+        for (int it = 0; it < Lay::kItems; ++it) {
+            const int q = lane + it * kWave;
+            if (q < kChunk * F4) reinterpret_cast<float4 *>(raw + c * kChunk * N)[q] = st.x[c][it];
+        }
+#pragma unroll
+    for (int it = 0; it < Lay::kVItems; ++it) {
+        const int q = lane + it * kWave;
+        if (q < kChunk * Lay::kVF4) reinterpret_cast<float4 *>(vbuf)[q] = st.v[it];
+    }
+    if constexpr (PREP) {
+        // Per-token L2 norm of k * k_k over the head (F.normalize, eps 1e-12):
+        // partial sums of squares per 4 columns, then one lane per token.
+#pragma unroll
+        for (int it = 0; it < Lay::kItems; ++it) {
+            const int q = lane + it * kWave;
+            if (q < kChunk * F4) {
+                const int f = q - (q / F4) * F4;
+                const float4 kv = st.x[kRawK][it];
+                const float4 kk = *reinterpret_cast<const float4 *>(p.k_k + h * N + f * 4);
+                const float x0 = kv.x * kk.x, x1 = kv.y * kk.y, x2 = kv.z * kk.z, x3 = kv.w * kk.w;
+                psq[q] = fmaf(x0, x0, fmaf(x1, x1, fmaf(x2, x2, x3 * x3)));
             }
         }
-        __syncthreads();
+        lds_barrier();
         if (lane < nt) {
             float acc = 0.0f;
-            for (int j = 0; j < N; ++j) acc += sq[lane * N + j];
+            for (int f = 0; f < F4; ++f) acc += psq[lane * F4 + f];
             inv_norm[lane] = 1.0f / fmaxf(sqrtf(acc), 1e-12f);
         }
-        __syncthreads();
     }
+    lds_barrier();
+    for (int q = lane; q < nt * F4; q += kWave) {
+        const int t = q / F4, f = q - t * F4;
+        const float4 r4 = reinterpret_cast<const float4 *>(raw + kRawR * kChunk * N)[q];
+        const float4 w4 = reinterpret_cast<const float4 *>(raw + kRawW * kChunk * N)[q];
+        const float4 k4 = reinterpret_cast<const float4 *>(raw + kRawK * kChunk * N)[q];
+        const float4 a4 = reinterpret_cast<const float4 *>(raw + kRawA * kChunk * N)[q];
+        float4 b4 = a4;
+        if constexpr (!PREP) b4 = reinterpret_cast<const float4 *>(raw + kRawB * kChunk * N)[q];
+        const float rr[4] = {r4.x, r4.y, r4.z, r4.w}, ww[4] = {w4.x, w4.y, w4.z, w4.w};
+        const float kk[4] = {k4.x, k4.y, k4.z, k4.w}, aa[4] = {a4.x, a4.y, a4.z, a4.w};
+        const float bb[4] = {b4.x, b4.y, b4.z, b4.w};
 #pragma unroll
-    for (int it = 0; it < Lay::kItems; ++it) {
-        const int q = lane + it * kWave;
-        const int t = q / N, j = q - t * N;
-        if (q < kChunk * N && t < nt) {
+        for (int u = 0; u < 4; ++u) {
+            const int j = f * 4 + u;
+            // d = exp(-e^{-0.5} sigmoid(w)) = exp2(-e^{-0.5} log2(e) sigmoid(w)).
+            const float sig = __frcp_rn(1.0f + __expf(-ww[u]));
+            const float dv = exp2f(-0.8750387749f * sig);
             float av, bv, kv;
             if constexpr (PREP) {
-                const float kap = kk[it] * inv_norm[t];
-                const float alpha = st.a[it];
+                const float kap = kk[u] * p.k_k[h * N + j] * inv_norm[t];
                 av = -kap;
-                bv = kap * alpha;
-                kv = st.k[it] * (1.0f + (alpha - 1.0f) * p.k_a[h * N + j]);
+                bv = kap * aa[u];
+                kv = kk[u] * (1.0f + (aa[u] - 1.0f) * p.k_a[h * N + j]);
             } else {
-                av = st.a[it];
-                bv = st.b[it];
-                kv = st.k[it];
+                av = aa[u];
+                bv = bb[u];
+                kv = kk[u];
             }
-            const float dv = expf(-kWScale / (1.0f + expf(-st.w[it])));
             const int cl = j / E, e = j - cl * E;
             float *dst = cols + (t * L + cl) * P + e;
             dst[kA * E] = av;
             dst[kD * E] = dv;
             dst[kB * E] = bv;
             dst[kK * E] = kv;
-            dst[kR * E] = st.r[it];
+            dst[kR * E] = rr[u];
         }
     }
-#pragma unroll
-    for (int it = 0; it < Lay::kVItems; ++it) {
-        const int q = lane + it * kWave;
-        if (q < kChunk * Lay::R) vbuf[q] = st.v[it];
-    }
+    lds_barrier();
 }
 
 template <int N>
@@ -213,10 +240,11 @@ template <int N, bool PREP>
 __global__ void __launch_bounds__(kWave) wkv7_scan_kernel(WkvParams p, int waves_total, int per_xcd) {
     using Lay = Layout<N>;
     constexpr int E = Lay::E, L = Lay::L, R = Lay::R, W = Lay::W;
-    __shared__ __attribute__((aligned(16))) float cols[2][Lay::kCols];
-    __shared__ float vbuf[2][kChunk * R];
+    __shared__ __attribute__((aligned(16))) float raw[kNumRaw * kChunk * N];
+    __shared__ __attribute__((aligned(16))) float cols[Lay::kCols];
+    __shared__ __attribute__((aligned(16))) float vbuf[kChunk * R];
     __shared__ float ybuf[kChunk * R];
-    __shared__ float sq[PREP ? kChunk * N : 1];
+    __shared__ float psq[PREP ? kChunk * Lay::kF4 : 1];
     __shared__ float inv_norm[kChunk];
 
     // XCD-aware flat index: blocks are dealt round-robin over the XCDs, so
@@ -234,37 +262,40 @@ __global__ void __launch_bounds__(kWave) wkv7_scan_kernel(WkvParams p, int waves
     const size_t state_off = ((size_t)slot * p.H + h) * N * N;
 
     float s[E];
+    {
+        const auto rs = make_rsrc(p.state_in ? p.state_in + state_off : nullptr, p.state_in ? N * N * 4 : 0u);
 #pragma unroll
-    for (int e = 0; e < E; ++e)
-        s[e] = (p.state_in && row_ok) ? p.state_in[state_off + (size_t)i * N + cl * E + e] : 0.0f;
+        for (int e = 0; e < E; ++e)
+            s[e] = buf_load(rs, row_ok ? (uint32_t)(i * N + cl * E + e) * 4u : kBufferOob);
+    }
+    wait_vmem();
 
     const int n_chunks = (p.T + kChunk - 1) / kChunk;
-    Stage<N, PREP> st;
-    if (n_chunks > 0) {
-        const int nt0 = min(kChunk, p.T);
-        stage_load<N, PREP>(st, p, bb, h, row0, 0, nt0, lane);
-        stage_store<N, PREP>(st, p, h, nt0, lane, cols[0], vbuf[0], sq, inv_norm);
-    }
-    __syncthreads();
+    Stage<N> st;
+    if (n_chunks > 0) stage_load<N, PREP>(st, p, bb, h, row0, 0, min(kChunk, p.T), lane);
     for (int c = 0; c < n_chunks; ++c) {
         const int t0 = c * kChunk;
         const int nt = min(kChunk, p.T - t0);
-        const int buf = c & 1;
-        const bool more = c + 1 < n_chunks;
-        const int nt_next = more ? min(kChunk, p.T - t0 - kChunk) : 0;
-        if (more) stage_load<N, PREP>(st, p, bb, h, row0, t0 + kChunk, nt_next, lane);
+        stage_store<N, PREP>(st, p, h, nt, lane, raw, cols, vbuf, psq, inv_norm);
+        if (c + 1 < n_chunks) stage_load<N, PREP>(st, p, bb, h, row0, t0 + kChunk, min(kChunk, p.T - t0 - kChunk), lane);
         if (nt == kChunk)
-            chunk_steps<N, true>(s, cols[buf], vbuf[buf], ybuf, nt, rl, cl);
+            chunk_steps<N, true>(s, cols, vbuf, ybuf, nt, rl, cl);
         else
-            chunk_steps<N, false>(s, cols[buf], vbuf[buf], ybuf, nt, rl, cl);
-        __syncthreads();
-        // Write this chunk's outputs: R contiguous rows per token.
-        for (int q = lane; q < nt * R; q += kWave) {
-            const int t = q / R, rr = q - t * R;
-            if (row0 + rr < N) p.y[((size_t)(bb * p.T + t0 + t) * p.H + h) * N + row0 + rr] = ybuf[q];
+            chunk_steps<N, false>(s, cols, vbuf, ybuf, nt, rl, cl);
+        lds_barrier();
+        // This chunk's outputs: R contiguous rows per token, stored through a
+        // buffer descriptor (stores past the chunk end or past row N drop).
+        {
+            const size_t ybase = ((size_t)(bb * p.T + t0) * p.H + h) * N;
+            const auto ry = make_rsrc(p.y + ybase, (uint32_t)(((nt - 1) * p.H * N + N) * 4));
+#pragma unroll
+            for (int it = 0; it < (kChunk * R + kWave - 1) / kWave; ++it) {
+                const int q = lane + it * kWave;
+                const int t = q / R, rr = q - t * R;
+                const bool ok = q < kChunk * R && t < nt && row0 + rr < N;
+                buf_store(ybuf[ok ? q : 0], ry, ok ? (uint32_t)(t * p.H * N + row0 + rr) * 4u : kBufferOob);
+            }
         }
-        if (more) stage_store<N, PREP>(st, p, h, nt_next, lane, cols[buf ^ 1], vbuf[buf ^ 1], sq, inv_norm);
-        __syncthreads();
     }
     if (p.state_out && row_ok) {
 #pragma unroll
