@@ -5,14 +5,16 @@
 //     m_t    = lambda * H(m_{t-1}) + sigmoid(write_t) * tanh(cand_t)
 //     read_t = H(m_t) [* sigmoid(read_raw_t)],     H(x) = x - 2 (x.u) u.
 //
-// Design: one wave per stream; a lane owns D / 64 memory channels (strided,
-// so every per-token HBM access is a coalesced 256 B row).  The reference
-// kernel recomputes two O(D) dot products in every thread for every token
-// (O(D^2) work per token); here each token needs exactly ONE wave reduction,
-// because the projection used by the read at token t, m_t.u, is also the
-// projection the update at token t+1 needs.  The write term and the read gate
-// are computed in the 16-token staging pass (off the sequential chain), and the
-// next chunk's pre-activations are loaded while the current chunk runs.
+// Design: one 4-wave workgroup per stream.  Wave 0 runs the sequential chain
+// and nothing else: per token one FMA pair per channel, ONE wave reduction (the
+// projection m_t.u serves both the read of token t and the update of token
+// t+1 -- the reference recomputes two O(D) dot products in every thread), the
+// gated read and a buffer store.  Waves 1-3 are producers: while wave 0 runs
+// chunk c they load chunk c+1's pre-activations from HBM and turn them into
+// the write term sigmoid(w) tanh(c) and the gate sigmoid(rho) in LDS (double
+// buffered), so no transcendental and no HBM latency sits on the chain.  Chunk
+// length is 32 tokens for D <= 256 and shrinks for wider memories so the two
+// LDS buffers stay within 128 KB.
 #include "common.h"
 #include "kernels.h"
 
@@ -20,101 +22,109 @@ namespace yuf {
 namespace {
 
 constexpr int kWave = 64;
-// Tokens per staging chunk: 16, fewer for wide memories to bound registers.
-template <int EPL>
-constexpr int chunk_len() { return EPL <= 2 ? 16 : 32 / EPL; }
+constexpr int kWaves = 4;
+constexpr int kProducers = (kWaves - 1) * kWave;
 
 template <int EPL>
-__global__ void __launch_bounds__(kWave) rosa_scan_kernel(RosaParams p) {
-    constexpr int kChunk = chunk_len<EPL>();
+constexpr int chunk_len() { return EPL <= 4 ? 32 : 64 / EPL; }
+
+template <int EPL>
+__global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p) {
+    constexpr int C = chunk_len<EPL>();
+    constexpr int DP = EPL * kWave;  // padded channel count
+    // [buffer][token][channel] write term and read gate.
+    __shared__ __attribute__((aligned(16))) float ew[2][C * DP];
+    __shared__ __attribute__((aligned(16))) float gt[2][C * DP];
+
     const int bb = blockIdx.x;
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int D = p.D;
     const int slot = p.slot ? p.slot[bb] : bb;
-
-    float lam[EPL], u[EPL], m[EPL];
-    // Direction and decay.  Model path: u = householder / max(|householder|, 1e-12),
-    // lambda = sigmoid(decay_param) (model.py:300-301).
-    float nrm = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        const int c = lane + e * kWave;
-        const bool ok = c < D;
-        u[e] = ok ? p.direction[c] : 0.0f;
-        lam[e] = ok ? p.decay[c] : 0.0f;
-        m[e] = (ok && p.memory_in) ? p.memory_in[(size_t)slot * D + c] : 0.0f;
-        nrm = fmaf(u[e], u[e], nrm);
-    }
-    if (p.raw_params) {
-        const float inv = 1.0f / fmaxf(sqrtf(wave_sum(nrm)), 1e-12f);
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            u[e] *= inv;
-            lam[e] = 1.0f / (1.0f + expf(-lam[e]));
-        }
-    }
-    // Projection of the incoming memory.
-    float proj = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) proj = fmaf(m[e], u[e], proj);
-    proj = wave_sum(proj);
-
     const bool gated = p.read_raw != nullptr;
-    float pc[kChunk][EPL], pw[kChunk][EPL], pr[kChunk][EPL];
-    auto load_chunk = [&](int t0, int nt) {
-        // Rows past the chunk end and channels past D fall outside the buffer
-        // descriptors and load as 0, so they contribute nothing to reductions.
+    const int n_chunks = (p.T + C - 1) / C;
+
+    // Producers: chunk -> LDS buffer.  Channels past D and tokens past T are 0.
+    auto produce = [&](int ch, int buf) {
+        const int t0 = ch * C, nt = min(C, p.T - t0);
         const size_t base = (size_t)(bb * p.T + t0) * p.ld;
-        const uint32_t bytes = nt > 0 ? (uint32_t)(((nt - 1) * p.ld + D) * 4) : 0u;
+        const uint32_t bytes = (uint32_t)(((nt - 1) * p.ld + D) * 4);
         const auto rc = make_rsrc(p.cand + base, bytes), rw = make_rsrc(p.write + base, bytes);
         const auto rr = make_rsrc(gated ? p.read_raw + base : p.cand + base, gated ? bytes : 0u);
-#pragma unroll
-        for (int t = 0; t < kChunk; ++t) {
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int c = lane + e * kWave;
-                const uint32_t off = c < D ? (uint32_t)(t * p.ld + c) * 4u : kBufferOob;
-                pc[t][e] = buf_load(rc, off);
-                pw[t][e] = buf_load(rw, off);
-                pr[t][e] = buf_load(rr, off);
-            }
+        for (int q = tid - kWave; q < C * DP; q += kProducers) {
+            const int t = q / DP, c = q - t * DP;
+            const uint32_t off = (c < D && t < nt) ? (uint32_t)(t * p.ld + c) * 4u : kBufferOob;
+            const float cv = buf_load(rc, off), wv = buf_load(rw, off), rv = buf_load(rr, off);
+            // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).
+            const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * cv) + 1.0f);
+            ew[buf][q] = th * __frcp_rn(1.0f + __expf(-wv));
+            gt[buf][q] = gated ? __frcp_rn(1.0f + __expf(-rv)) : 1.0f;
         }
     };
-    const int n_chunks = (p.T + kChunk - 1) / kChunk;
-    if (n_chunks > 0) load_chunk(0, min(kChunk, p.T));
-    for (int ch = 0; ch < n_chunks; ++ch) {
-        const int t0 = ch * kChunk;
-        const int nt = min(kChunk, p.T - t0);
-        // Off-chain transforms of this chunk: write term and read gate.
-        float ew[kChunk][EPL], g[kChunk][EPL];
+
+    // Consumer state: lane owns channels lane + 64 e.
+    float lam[EPL], u[EPL], m[EPL];
+    float proj = 0.0f;
+    if (wave == 0) {
+        float nrm = 0.0f;
 #pragma unroll
-        for (int t = 0; t < kChunk; ++t) {
+        for (int e = 0; e < EPL; ++e) {
+            const int c = lane + e * kWave;
+            const bool ok = c < D;
+            u[e] = ok ? p.direction[c] : 0.0f;
+            lam[e] = ok ? p.decay[c] : 0.0f;
+            m[e] = (ok && p.memory_in) ? p.memory_in[(size_t)slot * D + c] : 0.0f;
+            nrm = fmaf(u[e], u[e], nrm);
+        }
+        if (p.raw_params) {
+            // Model path: u = householder / max(|householder|, 1e-12), lambda = sigmoid(decay)
+            // (model.py:300-301).
+            const float inv = 1.0f / fmaxf(sqrtf(wave_sum(nrm)), 1e-12f);
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).
-                const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * pc[t][e]) + 1.0f);
-                ew[t][e] = th * __frcp_rn(1.0f + __expf(-pw[t][e]));
-                g[t][e] = gated ? __frcp_rn(1.0f + __expf(-pr[t][e])) : 1.0f;
+                u[e] *= inv;
+                lam[e] = 1.0f / (1.0f + expf(-lam[e]));
             }
         }
-        if (ch + 1 < n_chunks) load_chunk(t0 + kChunk, min(kChunk, p.T - t0 - kChunk));
-        for (int t = 0; t < nt; ++t) {
-            float q = 0.0f;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                m[e] = fmaf(lam[e], m[e] - 2.0f * proj * u[e], ew[t][e]);
-                q = fmaf(m[e], u[e], q);
-            }
-            proj = wave_sum(q);
-            const size_t row = (size_t)(bb * p.T + t0 + t) * D;
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int c = lane + e * kWave;
-                if (c < D) p.read_out[row + c] = (m[e] - 2.0f * proj * u[e]) * g[t][e];
-            }
-        }
+        for (int e = 0; e < EPL; ++e) proj = fmaf(m[e], u[e], proj);
+        proj = wave_sum(proj);
+        wait_vmem();
+    } else if (n_chunks > 0) {
+        produce(0, 0);
     }
-    if (p.memory_out) {
+    lds_barrier();
+
+    for (int ch = 0; ch < n_chunks; ++ch) {
+        const int buf = ch & 1;
+        if (wave == 0) {
+            const int t0 = ch * C, nt = min(C, p.T - t0);
+            const size_t obase = (size_t)(bb * p.T + t0) * D;
+            const auto ro = make_rsrc(p.read_out + obase, (uint32_t)(nt * D * 4));
+            const float *e_row = ew[buf] + lane;
+            const float *g_row = gt[buf] + lane;
+            for (int t = 0; t < nt; ++t) {
+                float q = 0.0f;
+                const float two_p = 2.0f * proj;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    m[e] = fmaf(lam[e], fmaf(-two_p, u[e], m[e]), e_row[t * DP + e * kWave]);
+                    q = fmaf(m[e], u[e], q);
+                }
+                proj = wave_sum(q);
+                const float two_q = 2.0f * proj;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const int c = lane + e * kWave;
+                    const float rv = fmaf(-two_q, u[e], m[e]) * g_row[t * DP + e * kWave];
+                    buf_store(rv, ro, c < D ? (uint32_t)(t * D + c) * 4u : kBufferOob);
+                }
+            }
+        } else if (ch + 1 < n_chunks) {
+            produce(ch + 1, buf ^ 1);
+        }
+        lds_barrier();
+    }
+    if (wave == 0 && p.memory_out) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const int c = lane + e * kWave;
@@ -127,7 +137,7 @@ __global__ void __launch_bounds__(kWave) rosa_scan_kernel(RosaParams p) {
 
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
     if (p.B <= 0) return hipSuccess;
-    const dim3 grid(p.B), block(kWave);
+    const dim3 grid(p.B), block(kWaves * kWave);
     const int epl = (p.D + kWave - 1) / kWave;
     if (epl <= 1) hipLaunchKernelGGL(rosa_scan_kernel<1>, grid, block, 0, stream, p);
     else if (epl <= 2) hipLaunchKernelGGL(rosa_scan_kernel<2>, grid, block, 0, stream, p);
