@@ -141,6 +141,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["scan", "prefill"], default=None,
+                    help="profiling aid: run just the C2 scan (20 launches) or just the prefill steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -148,6 +150,10 @@ def main() -> int:
         return 2
 
     import torch
+
+    if args.only == "scan":
+        print(json.dumps({"roofline": bench_scan(20)}), flush=True)
+        return 0
 
     from yufmusicgen_amd.checkpoint import write_yuf
     from yufmusicgen_amd.config import PRESETS
@@ -186,6 +192,9 @@ def main() -> int:
     ms_per_step = elapsed * 1e3 / args.steps
     prefill_tps = B * T * args.steps / elapsed
     log(f"prefill {ms_per_step:.2f} ms/step, {prefill_tps:.0f} tokens/s")
+    if args.only == "prefill":
+        print(json.dumps({"prefill_tokens_per_s": prefill_tps, "ms_per_step": ms_per_step}), flush=True)
+        return 0
 
     # C4 decode: 64 streams x 256-token prefill, then decode with device top-k sampling.
     S, P = 64, 256

@@ -217,14 +217,32 @@ T *carve(char *&cursor, size_t count) {
     return p;
 }
 
-int gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C, int ldc,
-         const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr, int ldr = 0,
-         bool silu_pair = false) {
+GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C,
+                     int ldc, const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr,
+                     int ldr = 0, bool silu_pair = false) {
     GemmParams p;
     p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.C = C; p.ldc = ldc;
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = ldr; p.silu_pair = silu_pair;
     p.workspace = e.gemm_ws; p.workspace_floats = e.gemm_ws_floats;
-    ENG_TRY(launch_gemm(p, e.stream), "gemm");
+    return p;
+}
+
+int gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C, int ldc,
+         const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr, int ldr = 0,
+         bool silu_pair = false) {
+    ENG_TRY(launch_gemm(make_gemm(e, M, N, K, A, lda, W, ldw, C, ldc, bias, act, residual, ldr, silu_pair), e.stream),
+            "gemm");
+    return YUF_OK;
+}
+
+// Several independent products in one launch (the short-M split-K path runs
+// them one after another: its workspace holds one product at a time).
+int gemm_group(Engine &e, const GemmParams *ps, int count) {
+    if (ps[0].M <= 64) {
+        for (int i = 0; i < count; ++i) ENG_TRY(launch_gemm(ps[i], e.stream), "gemm");
+        return YUF_OK;
+    }
+    ENG_TRY(launch_gemm_group(ps, count, e.stream), "gemm group");
     return YUF_OK;
 }
 
@@ -248,15 +266,22 @@ int forward_pass(Engine &e, int n, int Tc, float *logits, int mode, int row_stri
         const float *mr = e.mix, *mw = e.mix + plane, *mk = e.mix + 2 * plane, *mv = e.mix + 3 * plane,
                     *ma = e.mix + 4 * plane, *mg = e.mix + 5 * plane;
         int rc;
-        if ((rc = gemm(e, M, d, d, mr, d, w.w_r, d, e.r, d)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, d, d, mk, d, w.w_k, d, e.k, d)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, d, d, mv, d, w.w_v, d, e.v, d)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, L, d, mw, d, w.w1t, d, e.lr, L, nullptr, ACT_TANH)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, d, L, e.lr, L, w.w2t, L, e.wr, d, w.w0)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, L, d, ma, d, w.a1t, d, e.lr, L)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, d, L, e.lr, L, w.a2t, L, e.al, d, w.a0, ACT_SIGMOID)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, L, d, mg, d, w.g1t, d, e.lr, L)) != YUF_OK) return rc;
-        if ((rc = gemm(e, M, d, L, e.lr, L, w.g2t, L, e.g, d, nullptr, ACT_SIGMOID)) != YUF_OK) return rc;
+        {
+            // r, k, v in one launch; then the three low-rank first stages; then the second stages.
+            const float *lw = e.lr, *la = e.lr + (size_t)e.max_tokens * L, *lg = e.lr + 2 * (size_t)e.max_tokens * L;
+            GemmParams g3[3] = {make_gemm(e, M, d, d, mr, d, w.w_r, d, e.r, d),
+                                make_gemm(e, M, d, d, mk, d, w.w_k, d, e.k, d),
+                                make_gemm(e, M, d, d, mv, d, w.w_v, d, e.v, d)};
+            if ((rc = gemm_group(e, g3, 3)) != YUF_OK) return rc;
+            GemmParams l1[3] = {make_gemm(e, M, L, d, mw, d, w.w1t, d, const_cast<float *>(lw), L, nullptr, ACT_TANH),
+                                make_gemm(e, M, L, d, ma, d, w.a1t, d, const_cast<float *>(la), L),
+                                make_gemm(e, M, L, d, mg, d, w.g1t, d, const_cast<float *>(lg), L)};
+            if ((rc = gemm_group(e, l1, 3)) != YUF_OK) return rc;
+            GemmParams l2[3] = {make_gemm(e, M, d, L, lw, L, w.w2t, L, e.wr, d, w.w0),
+                                make_gemm(e, M, d, L, la, L, w.a2t, L, e.al, d, w.a0, ACT_SIGMOID),
+                                make_gemm(e, M, d, L, lg, L, w.g2t, L, e.g, d, nullptr, ACT_SIGMOID)};
+            if ((rc = gemm_group(e, l2, 3)) != YUF_OK) return rc;
+        }
         WkvParams wp;
         wp.B = n; wp.T = Tc; wp.H = s.heads;
         wp.r = e.r; wp.w = e.wr; wp.k = e.k; wp.v = e.v; wp.a = e.al;
@@ -430,7 +455,7 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
     }
     e.gemm_ws_floats = ws;
     const size_t sizes[] = {Mx * d, Mx * d, 6 * Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d,
-                            Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
+                            3 * Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
                             (size_t)max_streams * d, ws};
     size_t total = 0;
     for (size_t z : sizes) total += ((z * sizeof(float) + 255) / 256) * 256;

@@ -80,13 +80,21 @@ __device__ __forceinline__ float apply_act(float x, int act) {
     return x;
 }
 
-__global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmParams p, int tiles_m, int tiles_n, int per_xcd) {
+struct GemmGroup {
+    GemmParams p[kMaxGroup];
+    int tiles_n[kMaxGroup];
+    int total[kMaxGroup];
+};
+
+// blockIdx.y selects the product of a group; blockIdx.x its output tile.
+__global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmGroup g, int per_xcd) {
     __shared__ __attribute__((aligned(16))) float As[2][kBM * kLd];
     __shared__ __attribute__((aligned(16))) float Bs[2][kBN * kLd];
 
-    const int total = tiles_m * tiles_n;
+    const GemmParams &p = g.p[blockIdx.y];
+    const int tiles_n = g.tiles_n[blockIdx.y];
     const int flat = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    if (flat >= total) return;
+    if (flat >= g.total[blockIdx.y]) return;
     const int bm = flat / tiles_n, bn = flat - bm * tiles_n;
     const int m0 = bm * kBM, n0 = bn * kBN;
 
@@ -369,11 +377,33 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
         }
         return hipGetLastError();
     }
-    const int tiles_m = (p.M + kBM - 1) / kBM, tiles_n = (p.N + kBN - 1) / kBN;
-    const int total = tiles_m * tiles_n;
-    const int per_xcd = (total + kXcds - 1) / kXcds;
-    hipLaunchKernelGGL(gemm_f32_kernel, dim3(per_xcd * kXcds), dim3(kThreads), 0, stream, p, tiles_m, tiles_n,
-                       per_xcd);
+    return launch_gemm_group(&p, 1, stream);
+}
+
+hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream) {
+    if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
+    GemmGroup g{};
+    int max_total = 0, n = 0;
+    for (int i = 0; i < count; ++i) {
+        const GemmParams &p = ps[i];
+        if (p.M <= 0 || p.N <= 0) continue;
+        if (p.M <= 64) {  // short-M products take the split-K path one by one
+            hipError_t e = launch_gemm(p, stream);
+            if (e != hipSuccess) return e;
+            continue;
+        }
+        if (p.K <= 0 || p.lda < p.K || p.ldw < p.K) return hipErrorInvalidValue;
+        if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
+        if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
+        g.p[n] = p;
+        g.tiles_n[n] = (p.N + kBN - 1) / kBN;
+        g.total[n] = ((p.M + kBM - 1) / kBM) * g.tiles_n[n];
+        max_total = std::max(max_total, g.total[n]);
+        ++n;
+    }
+    if (n == 0) return hipSuccess;
+    const int per_xcd = (max_total + kXcds - 1) / kXcds;
+    hipLaunchKernelGGL(gemm_f32_kernel, dim3(per_xcd * kXcds, n), dim3(kThreads), 0, stream, g, per_xcd);
     return hipGetLastError();
 }
 

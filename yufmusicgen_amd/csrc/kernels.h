@@ -66,6 +66,9 @@ struct GemmParams {
     size_t workspace_floats = 0;
 };
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
+// Up to kMaxGroup independent products in one launch (same path: M > 64).
+constexpr int kMaxGroup = 4;
+hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream);
 // Workspace the short-M path can use for an N-column product (floats).
 size_t gemm_workspace_floats(int N, int K);
 
