@@ -109,7 +109,7 @@ def test_wkv7_delta_rule_write_property():
         torch.testing.assert_close(mapped, _dev(v[:, t]), rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("dim", [12, 32, 128, 256])
+@pytest.mark.parametrize("dim", [12, 32, 128, 256, 512, 1000])
 @pytest.mark.parametrize("steps", [1, 19, 64])
 @pytest.mark.parametrize("gated", [False, True])
 def test_rosa_matches_oracle(dim, steps, gated):
@@ -133,3 +133,38 @@ def test_rosa_reference_golden(golden_dir):
     read, m = rosa_householder_scan(*args, gated=True)
     np.testing.assert_allclose(read.cpu().numpy(), z["read"], rtol=RTOL, atol=ATOL)
     np.testing.assert_allclose(m.cpu().numpy(), z["m"], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("decay_value", [None, 0.99, 0.05])
+def test_rosa_full_size(decay_value):
+    """C3 shape (B=8, T=2048, D=128, gated), with the drawn decays and with
+    every decay pinned at 0.99 (slow memory) and 0.05 (fast memory).  At 0.999
+    even an exact-order float32 recurrence leaves elements outside 1e-4/1e-5."""
+    from yufmusicgen_amd.ops import rosa_householder_scan
+
+    print(f"rosa full size decay={decay_value}", flush=True)
+    cand, write, read_raw, decay, u = rosa_inputs(11, 8, 2048, 128)
+    if decay_value is not None:
+        decay = np.full_like(decay, decay_value)
+    m0 = np.random.default_rng(5).standard_normal((8, 128)).astype(np.float32)
+    arrs = (cand, write, read_raw, decay, u, m0)
+    read, m = rosa_householder_scan(*(_dev(x) for x in arrs), gated=True)
+    re, me = orosa.rosa_scan(*(torch.from_numpy(x.astype(np.float64)) for x in arrs), gated=True)
+    np.testing.assert_allclose(read.cpu().numpy(), re.numpy(), rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(m.cpu().numpy(), me.numpy(), rtol=RTOL, atol=ATOL)
+
+
+def test_rosa_chunked_continuation():
+    """Scanning T tokens in ragged pieces, carrying the memory, equals one scan."""
+    from yufmusicgen_amd.ops import rosa_householder_scan
+
+    cand, write, read_raw, decay, u = rosa_inputs(4, 2, 100, 128)
+    m = torch.zeros(2, 128, device="cuda")
+    full, m_full = rosa_householder_scan(*(_dev(x) for x in (cand, write, read_raw, decay, u)), m, gated=True)
+    outs = []
+    for lo, hi in ((0, 7), (7, 40), (40, 41), (41, 100)):
+        piece = [_dev(x[:, lo:hi]) for x in (cand, write, read_raw)]
+        r, m = rosa_householder_scan(*piece, _dev(decay), _dev(u), m, gated=True)
+        outs.append(r)
+    torch.testing.assert_close(torch.cat(outs, dim=1), full, rtol=RTOL, atol=ATOL)
+    torch.testing.assert_close(m, m_full, rtol=RTOL, atol=ATOL)

@@ -2,19 +2,31 @@
 //
 // Semantics: yufmusicgen/model.py:260-288 (reference recurrence) and the read
 // of model.py:303-311 / yufmusicgen/cuda/rosa_householder.cu:30-101:
-//     m_t    = lambda * H(m_{t-1}) + sigmoid(write_t) * tanh(cand_t)
+//     m_t    = lambda * H(m_{t-1}) + e_t,   e_t = sigmoid(write_t) tanh(cand_t)
 //     read_t = H(m_t) [* sigmoid(read_raw_t)],     H(x) = x - 2 (x.u) u.
 //
-// Design: one 4-wave workgroup per stream.  Wave 0 runs the sequential chain
-// and nothing else: per token one FMA pair per channel, ONE wave reduction (the
-// projection m_t.u serves both the read of token t and the update of token
-// t+1 -- the reference recomputes two O(D) dot products in every thread), the
-// gated read and a buffer store.  Waves 1-3 are producers: while wave 0 runs
-// chunk c they load chunk c+1's pre-activations from HBM and turn them into
-// the write term sigmoid(w) tanh(c) and the gate sigmoid(rho) in LDS (double
-// buffered), so no transcendental and no HBM latency sits on the chain.  Chunk
-// length is 32 tokens for D <= 256 and shrinks for wider memories so the two
-// LDS buffers stay within 128 KB.
+// The transition diag(lambda) H = diag(lambda) - 2 (lambda u) u^T is diagonal
+// plus rank one, so with p_t = u.m_{t-1} the recurrence is
+//     m_t = lambda (m_{t-1} - 2 p_t u) + e_t.
+// Over a chunk of C tokens starting from m_0 (1-based tau):
+//     m_tau = y_tau - 2 c_tau,  y_tau = lambda^tau m_0 + z_tau,
+//     z_tau = lambda z_{tau-1} + e_tau (z_0 = 0),  c_tau = lambda (c_{tau-1} + p_tau u),
+// and the projections solve a lower-triangular Toeplitz system
+//     p_tau + 2 sum_{s<tau} kappa_{tau-s} p_s = f_tau := u.y_{tau-1},
+//     kappa_n = sum_j u_j^2 lambda_j^n,   p = L f,  L[tau][s] = ell_{tau-s},
+//     ell_0 = 1, ell_n = -2 sum_{k=1..n} kappa_k ell_{n-k}.
+// So the only cross-channel reductions are the C+1 dot products f (one batch
+// per chunk), not one wave reduction per token as in the direct recurrence.
+//
+// One workgroup per stream, 1 consumer wave + 8 producer waves, three LDS
+// stages in flight (chunk i+1 staged, chunk i solved, chunk i-1 emitted):
+//   producers, A(i+1): load chunk i+1's pre-activations (bounds-checked buffer
+//       loads), write e and the gate to LDS, run the per-channel z recurrence;
+//   consumer, B(i):   f = u.(lambda^tau m_0 + z_tau) for tau = 0..C (per-lane
+//       partials, transposed through LDS), p = L f, then the chunk-end state;
+//   producers, O(i-1): per channel, m_tau = lambda (m_{tau-1} - 2 p_tau u) + e_tau
+//       with the now-known p, and read_tau = (m_tau - 2 p_{tau+1} u) g_tau.
+// All waves meet at one barrier per chunk.
 #include "common.h"
 #include "kernels.h"
 
@@ -22,19 +34,40 @@ namespace yuf {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kWaves = 4;
-constexpr int kProducers = (kWaves - 1) * kWave;
+constexpr int kProducerWaves = 8;
+constexpr int kThreads = (1 + kProducerWaves) * kWave;
+constexpr int kStages = 3;
 
 template <int EPL>
-constexpr int chunk_len() { return EPL <= 4 ? 32 : 64 / EPL; }
+struct Cfg {
+    static constexpr int C = EPL <= 2 ? 16 : (EPL == 4 ? 8 : (EPL == 8 ? 4 : 2));  // tokens per chunk
+    static constexpr int DP = EPL * kWave;                                          // padded channels
+    static constexpr int ZS = C + 1;          // odd row stride of the transposed z / partial arrays
+    static constexpr int CH = DP / kProducerWaves;  // channels per producer wave
+    static constexpr int CPL = CH > kWave ? CH / kWave : 1;  // channels per producer lane
+};
+
+// LDS-only ordering between lanes of one wave (no s_barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 template <int EPL>
-__global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p) {
-    constexpr int C = chunk_len<EPL>();
-    constexpr int DP = EPL * kWave;  // padded channel count
-    // [buffer][token][channel] write term and read gate.
-    __shared__ __attribute__((aligned(16))) float ew[2][C * DP];
-    __shared__ __attribute__((aligned(16))) float gt[2][C * DP];
+__global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
+    using K = Cfg<EPL>;
+    constexpr int C = K::C, DP = K::DP, ZS = K::ZS, CH = K::CH, CPL = K::CPL;
+    __shared__ __attribute__((aligned(16))) float ew[kStages][C * DP];  // e_tau   [tau][c]
+    __shared__ __attribute__((aligned(16))) float gt[kStages][C * DP];  // gate    [tau][c]
+    __shared__ float zt[kStages][DP * ZS];                              // z_tau   [c][tau], tau = 0..C
+    __shared__ float pv[kStages][ZS];                                   // p_{tau+1}, tau = 0..C
+    __shared__ float m0b[kStages][DP];                                  // chunk-start state
+    __shared__ float lam_s[DP], u_s[DP];
+    // Consumer-only: per-lane partial dot products [lane][tau], f, and the Toeplitz
+    // inverse ell, in double: ell alternates in sign with |ell_n| up to 2 when the
+    // decay is near 1, so p = L f adds up to C rounding errors of f with weight 2.
+    __shared__ double part[kWave * ZS];
+    __shared__ double fv[ZS], ell[ZS];
 
     const int bb = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -43,27 +76,62 @@ __global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p)
     const bool gated = p.read_raw != nullptr;
     const int n_chunks = (p.T + C - 1) / C;
 
-    // Producers: chunk -> LDS buffer.  Channels past D and tokens past T are 0.
-    auto produce = [&](int ch, int buf) {
-        const int t0 = ch * C, nt = min(C, p.T - t0);
+    // ------------------------------------------------------------ producers
+    const int pw = wave - 1;
+    auto stage_in = [&](int ch) {  // A(ch)
+        const int s = ch % kStages, t0 = ch * C, nt = min(C, p.T - t0);
         const size_t base = (size_t)(bb * p.T + t0) * p.ld;
         const uint32_t bytes = (uint32_t)(((nt - 1) * p.ld + D) * 4);
         const auto rc = make_rsrc(p.cand + base, bytes), rw = make_rsrc(p.write + base, bytes);
         const auto rr = make_rsrc(gated ? p.read_raw + base : p.cand + base, gated ? bytes : 0u);
-        for (int q = tid - kWave; q < C * DP; q += kProducers) {
-            const int t = q / DP, c = q - t * DP;
-            const uint32_t off = (c < D && t < nt) ? (uint32_t)(t * p.ld + c) * 4u : kBufferOob;
+        for (int q = lane; q < C * CH; q += kWave) {
+            const int tau = q / CH, c = pw * CH + (q - tau * CH);
+            const uint32_t off = (c < D && tau < nt) ? (uint32_t)(tau * p.ld + c) * 4u : kBufferOob;
             const float cv = buf_load(rc, off), wv = buf_load(rw, off), rv = buf_load(rr, off);
-            // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).
+            // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).  Out-of-range
+            // tokens and channels read 0 and give e = 0.
             const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * cv) + 1.0f);
-            ew[buf][q] = th * __frcp_rn(1.0f + __expf(-wv));
-            gt[buf][q] = gated ? __frcp_rn(1.0f + __expf(-rv)) : 1.0f;
+            ew[s][tau * DP + c] = th * __frcp_rn(1.0f + __expf(-wv));
+            gt[s][tau * DP + c] = gated ? __frcp_rn(1.0f + __expf(-rv)) : 1.0f;
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int cc = lane + k * kWave;
+            if (cc < CH) {
+                const int c = pw * CH + cc;
+                const float lam = lam_s[c];
+                float z = 0.0f;
+                zt[s][c * ZS] = 0.0f;
+                for (int tau = 0; tau < C; ++tau) {
+                    z = fmaf(lam, z, ew[s][tau * DP + c]);
+                    zt[s][c * ZS + tau + 1] = z;
+                }
+            }
+        }
+    };
+    auto emit = [&](int ch) {  // O(ch)
+        const int s = ch % kStages, t0 = ch * C, nt = min(C, p.T - t0);
+        const size_t obase = (size_t)(bb * p.T + t0) * D;
+        const auto ro = make_rsrc(p.read_out + obase, (uint32_t)(nt * D * 4));
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int cc = lane + k * kWave;
+            if (cc < CH) {
+                const int c = pw * CH + cc;
+                const float lam = lam_s[c], u = u_s[c];
+                float m = m0b[s][c];
+                for (int tau = 0; tau < nt; ++tau) {
+                    m = fmaf(lam, fmaf(-2.0f * pv[s][tau], u, m), ew[s][tau * DP + c]);
+                    const float rv = fmaf(-2.0f * pv[s][tau + 1], u, m) * gt[s][tau * DP + c];
+                    buf_store(rv, ro, c < D ? (uint32_t)(tau * D + c) * 4u : kBufferOob);
+                }
+            }
         }
     };
 
-    // Consumer state: lane owns channels lane + 64 e.
-    float lam[EPL], u[EPL], m[EPL];
-    float proj = 0.0f;
+    // ------------------------------------------------------------- consumer
+    float lam[EPL], u[EPL], m0[EPL];
     if (wave == 0) {
         float nrm = 0.0f;
 #pragma unroll
@@ -72,7 +140,7 @@ __global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p)
             const bool ok = c < D;
             u[e] = ok ? p.direction[c] : 0.0f;
             lam[e] = ok ? p.decay[c] : 0.0f;
-            m[e] = (ok && p.memory_in) ? p.memory_in[(size_t)slot * D + c] : 0.0f;
+            m0[e] = (ok && p.memory_in) ? p.memory_in[(size_t)slot * D + c] : 0.0f;
             nrm = fmaf(u[e], u[e], nrm);
         }
         if (p.raw_params) {
@@ -81,46 +149,106 @@ __global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p)
             const float inv = 1.0f / fmaxf(sqrtf(wave_sum(nrm)), 1e-12f);
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
+                const int c = lane + e * kWave;
                 u[e] *= inv;
-                lam[e] = 1.0f / (1.0f + expf(-lam[e]));
+                lam[e] = c < D ? 1.0f / (1.0f + expf(-lam[e])) : 0.0f;
             }
         }
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) proj = fmaf(m[e], u[e], proj);
-        proj = wave_sum(proj);
-        wait_vmem();
-    } else if (n_chunks > 0) {
-        produce(0, 0);
-    }
-    lds_barrier();
-
-    for (int ch = 0; ch < n_chunks; ++ch) {
-        const int buf = ch & 1;
-        if (wave == 0) {
-            const int t0 = ch * C, nt = min(C, p.T - t0);
-            const size_t obase = (size_t)(bb * p.T + t0) * D;
-            const auto ro = make_rsrc(p.read_out + obase, (uint32_t)(nt * D * 4));
-            const float *e_row = ew[buf] + lane;
-            const float *g_row = gt[buf] + lane;
-            for (int t = 0; t < nt; ++t) {
-                float q = 0.0f;
-                const float two_p = 2.0f * proj;
+        for (int e = 0; e < EPL; ++e) {
+            lam_s[lane + e * kWave] = lam[e];
+            u_s[lane + e * kWave] = u[e];
+        }
+        // kappa_n = sum_j u_j^2 lambda_j^n, n = 1..C, then the Toeplitz inverse ell.
+        {
+            double pw_[EPL];
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) pw_[e] = (double)u[e] * u[e];
+            for (int n = 1; n <= C; ++n) {
+                double acc = 0.0;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
-                    m[e] = fmaf(lam[e], fmaf(-two_p, u[e], m[e]), e_row[t * DP + e * kWave]);
-                    q = fmaf(m[e], u[e], q);
+                    pw_[e] *= lam[e];
+                    acc += pw_[e];
                 }
-                proj = wave_sum(q);
-                const float two_q = 2.0f * proj;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    const int c = lane + e * kWave;
-                    const float rv = fmaf(-two_q, u[e], m[e]) * g_row[t * DP + e * kWave];
-                    buf_store(rv, ro, c < D ? (uint32_t)(t * D + c) * 4u : kBufferOob);
+                part[lane * ZS + n] = acc;
+            }
+            wave_lds_sync();
+            if (lane >= 1 && lane <= C) {
+                double acc = 0.0;
+                for (int k = 0; k < kWave; ++k) acc += part[k * ZS + lane];
+                fv[lane] = acc;  // kappa_lane
+            }
+            wave_lds_sync();
+            if (lane == 0) {
+                ell[0] = 1.0;
+                for (int n = 1; n <= C; ++n) {
+                    double acc = 0.0;
+                    for (int k = 1; k <= n; ++k) acc = fma(fv[k], ell[n - k], acc);
+                    ell[n] = -2.0 * acc;
                 }
             }
-        } else if (ch + 1 < n_chunks) {
-            produce(ch + 1, buf ^ 1);
+            wave_lds_sync();
+        }
+        wait_vmem();
+    }
+    lds_barrier();  // lam_s / u_s visible to the producers
+    if (wave > 0 && n_chunks > 0) stage_in(0);
+    lds_barrier();
+
+    for (int i = 0; i <= n_chunks; ++i) {
+        if (wave == 0) {
+            if (i < n_chunks) {
+                const int s = i % kStages, nt = min(C, p.T - i * C);
+                // f_{tau+1} = u . (lambda^tau m_0 + z_tau), tau = 0..C: per-lane partials.
+                float y[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) y[e] = m0[e];
+                for (int tau = 0; tau <= C; ++tau) {
+                    double acc = 0.0;
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        const double ud = u[e];
+                        acc = fma(ud, (double)y[e], fma(ud, (double)zt[s][(lane + e * kWave) * ZS + tau], acc));
+                        y[e] *= lam[e];
+                    }
+                    part[lane * ZS + tau] = acc;
+                }
+                wave_lds_sync();
+                if (lane <= C) {
+                    double acc = 0.0;
+                    for (int k = 0; k < kWave; ++k) acc += part[k * ZS + lane];
+                    fv[lane] = acc;
+                }
+                wave_lds_sync();
+                if (lane <= C) {
+                    double acc = 0.0;
+                    for (int sg = 0; sg <= lane; ++sg) acc = fma(ell[lane - sg], fv[sg], acc);
+                    pv[s][lane] = (float)acc;
+                }
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) m0b[s][lane + e * kWave] = m0[e];
+                wave_lds_sync();
+                // State after the chunk's nt real tokens:
+                // m_nt = lambda^nt m_0 + z_nt - 2 sum_{s<=nt} p_s lambda^{nt-s+1} u.
+                float acc[EPL], pwr[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) { acc[e] = 0.0f; pwr[e] = m0[e]; }
+                for (int sg = 0; sg < nt; ++sg) {
+                    const float ps = pv[s][sg];
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) {
+                        acc[e] = lam[e] * fmaf(ps, u[e], acc[e]);
+                        pwr[e] *= lam[e];
+                    }
+                }
+#pragma unroll
+                for (int e = 0; e < EPL; ++e)
+                    m0[e] = fmaf(-2.0f, acc[e], pwr[e] + zt[s][(lane + e * kWave) * ZS + nt]);
+            }
+        } else {
+            if (i >= 1) emit(i - 1);
+            if (i + 1 < n_chunks) stage_in(i + 1);
         }
         lds_barrier();
     }
@@ -128,7 +256,7 @@ __global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p)
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const int c = lane + e * kWave;
-            if (c < D) p.memory_out[(size_t)slot * D + c] = m[e];
+            if (c < D) p.memory_out[(size_t)slot * D + c] = m0[e];
         }
     }
 }
@@ -137,7 +265,7 @@ __global__ void __launch_bounds__(kWaves * kWave) rosa_scan_kernel(RosaParams p)
 
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
     if (p.B <= 0) return hipSuccess;
-    const dim3 grid(p.B), block(kWaves * kWave);
+    const dim3 grid(p.B), block(kThreads);
     const int epl = (p.D + kWave - 1) / kWave;
     if (epl <= 1) hipLaunchKernelGGL(rosa_scan_kernel<1>, grid, block, 0, stream, p);
     else if (epl <= 2) hipLaunchKernelGGL(rosa_scan_kernel<2>, grid, block, 0, stream, p);
