@@ -141,8 +141,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["scan", "prefill"], default=None,
-                    help="profiling aid: run just the C2 scan (20 launches) or just the prefill steps")
+    ap.add_argument("--only", choices=["scan", "prefill", "copy"], default=None,
+                    help="profiling aids: just the C2 scan (20 launches), just the prefill steps, or a plain "
+                         "256 MiB device copy (20 launches) that calibrates the FETCH_SIZE/WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -153,6 +154,12 @@ def main() -> int:
 
     if args.only == "scan":
         print(json.dumps({"roofline": bench_scan(20)}), flush=True)
+        return 0
+    if args.only == "copy":
+        src = torch.ones(64 << 20, device="cuda")
+        dst = torch.empty_like(src)
+        ms = time_events(lambda: dst.copy_(src), 20, torch.cuda.current_stream())
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "avg_us": round(ms * 1e3, 2)}), flush=True)
         return 0
 
     from yufmusicgen_amd.checkpoint import write_yuf
