@@ -218,6 +218,15 @@ int32_t yuf_sample(const float *logits, int V, float temperature, float top_p, i
 /* First index of the maximum (torch.argmax semantics). */
 int32_t yuf_argmax(const float *logits, int V);
 
+/* The generation loop's logit mask (vulkan/src/generation.rs:195-203,
+ * yufmusicgen/cli/generate.py:139-148): allowed_out[i] = logits[i] for MIDI
+ * ids i >= midi_offset, -inf elsewhere; ids midi_offset + blocked_raw_ids[j]
+ * are -inf; the EOS id keeps its logit once index >= min_before_eos (16 in
+ * the reference).  allowed_out may alias logits.  Host buffers [V]. */
+int yuf_generation_mask(const float *logits, int V, int index, int midi_offset, int eos_id,
+                        int min_before_eos, const int32_t *blocked_raw_ids, int n_blocked,
+                        float *allowed_out);
+
 /* Device sampling for n streams at once (no logits copy to the host):
  * temperature <= 0 -> argmax; otherwise top_k in [1, 64] largest scaled
  * logits, softmax over them and a Gumbel-max draw from a counter-based

@@ -66,6 +66,27 @@ def test_generation_mask_then_sample():
     assert got == expect and got >= 260
 
 
+@pytest.mark.parametrize("index", [0, 15, 16, 40])
+@pytest.mark.parametrize("blocked", [(), (0, 5, 127)])
+def test_native_generation_mask_matches_oracle(index, blocked):
+    from yufmusicgen_amd.engine import generation_mask as native_mask
+
+    x = np.random.default_rng(index).standard_normal(1000).astype(np.float32)
+    expect = generation_mask(torch.from_numpy(x), index=index, blocked_raw_ids=blocked).numpy()
+    np.testing.assert_array_equal(native_mask(x, index, blocked), expect)
+
+
+def test_native_generation_mask_rejects_bad_ids():
+    from yufmusicgen_amd._lib import YufError
+    from yufmusicgen_amd.engine import generation_mask as native_mask
+
+    x = np.zeros(300, np.float32)
+    with pytest.raises(YufError):
+        native_mask(x, 0, (40,))  # 260 + 40 >= V
+    with pytest.raises(YufError):
+        native_mask(x, 20, (), eos_id=300)
+
+
 def test_greedy_when_temperature_not_positive():
     x = np.array([0.1, 5.0, 2.0], np.float32)
     assert sample_token(x, 0.0, 0.95, Mt19937(1)) == 1

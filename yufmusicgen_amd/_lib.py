@@ -71,6 +71,8 @@ SIGNATURES = {
     "yuf_sample": (ctypes.c_int32, [c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_float, ctypes.c_int,
                                     ctypes.POINTER(RngC)]),
     "yuf_argmax": (ctypes.c_int32, [c_void_p, ctypes.c_int]),
+    "yuf_generation_mask": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, c_void_p, ctypes.c_int, c_void_p]),
     "yuf_sample_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_float, ctypes.c_int,
                                          ctypes.c_uint64, ctypes.c_uint64, c_void_p, c_void_p]),
 }

@@ -110,6 +110,27 @@ extern "C" int32_t yuf_argmax(const float *logits, int V) {
     return best;
 }
 
+extern "C" int yuf_generation_mask(const float *logits, int V, int index, int midi_offset, int eos_id,
+                                   int min_before_eos, const int32_t *blocked_raw_ids, int n_blocked,
+                                   float *allowed_out) {
+    if (!logits || !allowed_out || V <= 0) return yuf::fail(YUF_ERR_INVALID, "yuf_generation_mask: empty logits");
+    if (midi_offset < 0 || midi_offset > V) return yuf::fail(YUF_ERR_RANGE, "yuf_generation_mask: midi_offset outside [0, V]");
+    if (n_blocked < 0 || (n_blocked > 0 && !blocked_raw_ids))
+        return yuf::fail(YUF_ERR_INVALID, "yuf_generation_mask: bad blocked id list");
+    for (int j = 0; j < n_blocked; ++j)
+        if (blocked_raw_ids[j] < 0 || midi_offset + (int64_t)blocked_raw_ids[j] >= V)
+            return yuf::fail(YUF_ERR_RANGE, "yuf_generation_mask: blocked id outside the MIDI range");
+    if (index >= min_before_eos && (eos_id < 0 || eos_id >= V))
+        return yuf::fail(YUF_ERR_RANGE, "yuf_generation_mask: EOS id outside [0, V)");
+    const float eos_logit = (eos_id >= 0 && eos_id < V) ? logits[eos_id] : 0.0f;
+    for (int i = 0; i < midi_offset; ++i) allowed_out[i] = -INFINITY;
+    if (allowed_out != logits)
+        for (int i = midi_offset; i < V; ++i) allowed_out[i] = logits[i];
+    for (int j = 0; j < n_blocked; ++j) allowed_out[midi_offset + blocked_raw_ids[j]] = -INFINITY;
+    if (index >= min_before_eos) allowed_out[eos_id] = eos_logit;
+    return YUF_OK;
+}
+
 extern "C" int32_t yuf_sample(const float *logits, int V, float temperature, float top_p, int top_k, yuf_rng *rng) {
     if (!logits || V <= 0) return yuf::fail(YUF_ERR_INVALID, "yuf_sample: empty logits");
     if (!(temperature > 0.0f)) return yuf_argmax(logits, V);

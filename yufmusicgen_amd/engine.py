@@ -209,6 +209,19 @@ def argmax(logits) -> int:
     return int(out)
 
 
+def generation_mask(logits, index: int, blocked_raw_ids=(), midi_offset: int = 260, eos_id: int = 2,
+                    min_before_eos: int = 16) -> np.ndarray:
+    """The generation loop's mask (vulkan/src/generation.rs:195-203): MIDI ids
+    only, minus blocked Program ids, plus EOS from step ``min_before_eos``."""
+    arr = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.empty_like(arr)
+    blocked = np.ascontiguousarray(blocked_raw_ids, dtype=np.int32)
+    check(lib().yuf_generation_mask(arr.ctypes.data, arr.size, index, midi_offset, eos_id, min_before_eos,
+                                    blocked.ctypes.data if blocked.size else None, blocked.size,
+                                    out.ctypes.data))
+    return out
+
+
 def sample_device(logits_dev, tokens_dev, temperature: float, top_k: int, seed: int, counter: int, stream=None):
     """Top-k sampling of every row of ``logits_dev`` [n, V] on the GPU."""
     n, vocab = logits_dev.shape
