@@ -23,3 +23,11 @@ def pytest_configure(config):
 @pytest.fixture(scope="session")
 def golden_dir():
     return GOLDEN
+
+
+@pytest.fixture
+def wkv_kernel(request, monkeypatch):
+    """Force the per-token VALU WKV-7 kernel ("serial") or the chunked MFMA one
+    ("chunked"); the library reads YUF_WKV7_KERNEL at each launch."""
+    monkeypatch.setenv("YUF_WKV7_KERNEL", request.param)
+    return request.param

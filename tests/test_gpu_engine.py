@@ -34,7 +34,8 @@ def _states_from_blob(engine, slots):
     return np.stack([engine.save_state(s) for s in slots])
 
 
-def test_prefill_matches_reference_golden(state_test):
+@pytest.mark.parametrize("wkv_kernel", ["serial", "chunked"], indirect=True)
+def test_prefill_matches_reference_golden(state_test, wkv_kernel):
     ck, z = state_test
     eng = Engine(ck, max_streams=4, max_tokens=64)
     logits = eng.prefill(z["tokens"], logits="all")
@@ -53,7 +54,8 @@ def test_prefill_matches_reference_golden(state_test):
         np.testing.assert_allclose(s.rosa.numpy(), ref[f"state.{layer}.rosa"], rtol=1e-4, atol=1e-4)
 
 
-def test_continuation_from_carried_state_matches_reference(state_test):
+@pytest.mark.parametrize("wkv_kernel", ["serial", "chunked"], indirect=True)
+def test_continuation_from_carried_state_matches_reference(state_test, wkv_kernel):
     ck, z = state_test
     eng = Engine(ck, max_streams=2, max_tokens=64)
     head = eng.prefill(z["tokens"][:, :5], logits="all")

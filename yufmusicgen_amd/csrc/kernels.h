@@ -24,7 +24,12 @@ struct WkvParams {
     float *y = nullptr;  // [B, T, H, N]
 };
 bool wkv7_supported(int N);
+// Picks the chunked MFMA kernel (N <= 64, N % 4 == 0, T >= kWkvChunkMinT) or
+// the per-token VALU kernel; YUF_WKV7_KERNEL=serial|chunked forces one.
 hipError_t launch_wkv7(const WkvParams &p, int N, bool prep, hipStream_t stream);
+constexpr int kWkvChunkMinT = 32;
+bool wkv7_chunk_supported(int N);
+hipError_t launch_wkv7_chunked(const WkvParams &p, int N, bool prep, hipStream_t stream);
 
 // ------------------------------------------------------------------ ROSA scan
 struct RosaParams {

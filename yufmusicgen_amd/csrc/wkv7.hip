@@ -27,6 +27,9 @@
 //     kappa = normalize(k * k_k), a = -kappa, b = kappa * alpha and
 //     k_hat = k (1 + (alpha - 1) k_a) from the projections during staging
 //     (yufmusicgen/model.py:114-122), so the model path never materialises them.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -324,6 +327,11 @@ bool wkv7_supported(int N) {
 
 hipError_t launch_wkv7(const WkvParams &p, int N, bool prep, hipStream_t stream) {
     if (p.B <= 0 || p.H <= 0) return hipSuccess;
+    const char *force = std::getenv("YUF_WKV7_KERNEL");
+    const bool want_serial = force && std::strcmp(force, "serial") == 0;
+    const bool want_chunked = force && std::strcmp(force, "chunked") == 0;
+    if (wkv7_chunk_supported(N) && !want_serial && (want_chunked || p.T >= kWkvChunkMinT))
+        return launch_wkv7_chunked(p, N, prep, stream);
     switch (N) {
         case 8: return launch_n<8>(p, prep, stream);
         case 16: return launch_n<16>(p, prep, stream);

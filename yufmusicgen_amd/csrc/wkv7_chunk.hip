@@ -1,0 +1,471 @@
+// WKV-7 scan in chunk-parallel form on the fp32 matrix cores (gfx950 MFMA).
+//
+// Same recurrence as wkv7.hip (yufmusicgen/model.py:145-165): per (b, h)
+//     S_t = S_{t-1} (diag(d_t) + a_t b_t^T) + v_t k_t^T,   y_t = S_t r_t,
+// with d = exp(-e^{-0.5} sigmoid(w_raw)) in (0.545, 1].
+//
+// Chunk algebra (16 tokens, t = 0..15 inside the chunk; g_t = prod_{s<=t} d_s
+// per key column, g_{-1} = 1; S0 = state at the chunk start):
+//     A~_t = a_t g_{t-1},  R~_t = r_t g_t,  B^_t = b_t / g_t,  K^_t = k_t / g_t
+//     Gab = strict(A~ B^T),  P = strict(A~ K^T),  Qb = incl(R~ B^T),  Qk = incl(R~ K^T)
+//     U  = (I - Gab)^{-1} (A~ S0^T + P V)        rows u_t = S_{t-1} a_t  (the "sa" vectors)
+//     Y  = R~ S0^T + Qb U + Qk V                 rows y_t
+//     S_16^T = diag(g_15) (S0^T + B^^T U + K^^T V)
+// (U, Y as [token][value row]).  The decays enter only as sequential running
+// products in fp32 (4-token runs chained by their end products), so ratios g_t / g_s keep
+// their shared prefix exactly; a tree-shaped scan costs ~25% more error.
+// d >= 0.545 keeps 1/g below 2^14 inside a chunk.  An fp32 emulation of this
+// sequence stays within 0.65 of the 1e-4/1e-5 tolerance of the fp64
+// recurrence at C2 size.
+//
+// Work split for one head (one workgroup), NB = ceil(N/16) 16-row blocks:
+//   NB waves       consumers: wave q owns S^T[:, 16q..16q+15] as NB 16x16
+//                  accumulator tiles and runs the S-dependent products above,
+//                  16 NB + 16 v_mfma_f32_16x16x4f32 per chunk;
+//   one wave       stage B1: the four 16x16 Gram matrices (MFMA);
+//   NB waves       stage A: loads r, w, k, a, b, decays, running products and
+//                  the scaled operands -> LDS (16 columns each);
+//                  model path: kappa = normalize(k k_k), a = -kappa,
+//                  b = kappa alpha, k^ = k (1 + (alpha - 1) k_a) first;
+//   one wave       stage B2: (I - Gab)^{-1} by forward substitution, and in
+//                  the model path the per-token key norms of a later chunk.
+// Iteration i runs B2's norms on chunk i+4, A on i+3, B1 on i+2, B2's inverse
+// on i+1 and the consumers on chunk i, with one workgroup barrier per
+// iteration and ring buffers in LDS.  The consumers apply the chunk decay to
+// the state last:  S^T <- diag(g_15) (S0^T + B^^T U + K^^T V).
+//
+// MFMA operand layouts (16x16x4 f32; lane l, g = l / 16, li = l % 16):
+//   A operand A[m = li][k = g], B operand B[k = g][n = li],
+//   accumulator register r holds D[m = 4 g + r][n = li].
+// A product whose B operand is a previous accumulator uses k-step r to mean
+// rows {4 g + r}: register r of that accumulator is the B operand as is, and
+// the matching A operand is one ds_read_b128 of 4 consecutive k per lane.
+#include "common.h"
+#include "kernels.h"
+
+namespace yuf {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kC = 16;       // tokens per chunk
+constexpr int kWave = 64;
+constexpr int kXcds = 8;
+constexpr int kST = 20;      // row stride of 16-wide LDS tiles (floats, 16-byte aligned rows)
+
+__device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx4 ld4(const float *p) { return *reinterpret_cast<const floatx4 *>(p); }
+
+__device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, 0));
+}
+
+__device__ __forceinline__ void buf_store4(floatx4 v, __amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsrc, byte_offset, 0, 0);
+}
+
+template <int NB>
+struct Lds {
+    static constexpr int NP = 16 * NB;        // padded head size
+    static constexpr int SA = NP + 4;         // row stride of [token][column] tiles
+    // Ring A (4 chunks in flight): A~, R~ [16][SA]; B^^T, K^^T [NP][kST]; g_15 [NP].
+    static constexpr int oAs = 0, oRs = 16 * SA, oBhT = 32 * SA, oKhT = oBhT + NP * kST, oGl = oKhT + NP * kST;
+    static constexpr int kSlotA = oGl + NP;
+    // Ring H (2): B^, K^ [16][SA] (Gram inputs only).
+    static constexpr int oBh = 0, oKh = 16 * SA, kSlotH = 32 * SA;
+    // Ring G (3): Gab^T [s][t], P, Qb, Qk [t][s], all [16][kST].
+    static constexpr int oGabT = 0, oP = 16 * kST, oQb = 32 * kST, oQk = 48 * kST, kSlotG = 64 * kST;
+    // Ring T (2): (I - Gab)^{-1} [16][kST].
+    static constexpr int kSlotT = 16 * kST;
+    // Ring N (2): per-token 1 / max(|k k_k|, 1e-12) (model path).
+    static constexpr int kSlotN = 16;
+    static constexpr int kFloats = 4 * kSlotA + 2 * kSlotH + 3 * kSlotG + 2 * kSlotT + 2 * kSlotN;
+};
+
+// Wave roles.  Waves w and w + 4 of a workgroup share a SIMD, and a wave
+// issuing MFMAs halves the VALU issue rate of its SIMD neighbour, so each
+// MFMA-heavy wave (consumer or B1) is paired with one VALU-heavy wave
+// (stage A or B2): NB = 3 gives cons0+A0, cons1+A1, B1+B2, cons2+A2.
+enum : int { kRoleB1 = 8, kRoleB2 = 9, kRoleA = 12 };
+template <int NB> struct Roles {
+    static constexpr int kWaves = 2 * NB + 2;
+    __device__ static int of(int w) {
+        constexpr int A = kRoleA;
+        if constexpr (NB == 1) { constexpr int r[] = {0, kRoleB1, A, kRoleB2}; return r[w]; }
+        if constexpr (NB == 2) { constexpr int r[] = {0, 1, kRoleB1, A, A + 1, kRoleB2}; return r[w]; }
+        if constexpr (NB == 3) { constexpr int r[] = {0, 1, kRoleB1, 2, A, A + 1, kRoleB2, A + 2}; return r[w]; }
+        constexpr int r[] = {0, 1, 2, 3, A, A + 1, A + 2, A + 3, kRoleB1, kRoleB2};
+        return r[w];
+    }
+};
+
+__device__ __forceinline__ float lane_from(float x, int src_lane) {
+    return __int_as_float(__builtin_amdgcn_ds_bpermute((src_lane & 63) << 2, __float_as_int(x)));
+}
+
+template <int NB, bool PREP>
+__global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
+    wkv7_chunk_kernel(WkvParams p, int N, int heads, int per_xcd) {
+    using Ly = Lds<NB>;
+    using Ro = Roles<NB>;
+    constexpr int NP = Ly::NP, SA = Ly::SA;
+    __shared__ __attribute__((aligned(16))) float lds[Ly::kFloats];
+    float *ringA = lds;
+    float *ringH = ringA + 4 * Ly::kSlotA;
+    float *ringG = ringH + 2 * Ly::kSlotH;
+    float *ringT = ringG + 3 * Ly::kSlotG;
+    float *ringN = ringT + 2 * Ly::kSlotT;
+
+    // XCD-aware head index: consecutive heads of a batch row share an XCD's L2.
+    const int flat = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (flat >= heads) return;  // uniform over the workgroup
+    const int bb = flat / p.H, h = flat - bb * p.H;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int role = Ro::of(wave);
+    const int g = lane >> 4, li = lane & 15;
+    const int T = p.T, HN = p.H * N;
+    const int n_chunks = (T + kC - 1) / kC;
+    // Per-(b, h) token-major views: element (t, c) at t * HN + c.  Tokens past
+    // T fall outside the descriptor range and read as 0.
+    const size_t tok_base = ((size_t)bb * T * p.H + h) * N;
+    const uint32_t tok_bytes = T > 0 ? (uint32_t)(((size_t)(T - 1) * HN + N) * 4) : 0u;
+    const int chunk_bytes = kC * HN * 4;
+    const int slot = p.slot ? p.slot[bb] : bb;
+    const size_t state_off = ((size_t)slot * p.H + h) * N * N;
+
+    if (role < NB) {
+        // ------------------------------------------------------------ consumer
+        const int q = role;
+        const int i = 16 * q + li;  // value row owned by this lane's column of the tiles
+        floatx4 S[NB];
+        {
+            const auto rs = make_rsrc(p.state_in ? p.state_in + state_off : nullptr,
+                                      p.state_in ? (uint32_t)(N * N * 4) : 0u);
+#pragma unroll
+            for (int jb = 0; jb < NB; ++jb) {
+                const int j0 = 16 * jb + 4 * g;
+                S[jb] = buf_load4(rs, (i < N && j0 < N) ? (uint32_t)(i * N + j0) * 4u : kBufferOob);
+            }
+        }
+        const auto rv = make_rsrc(p.v + tok_base, tok_bytes);
+        const auto ry = make_rsrc(p.y + tok_base, tok_bytes);
+        float v[4];
+        auto load_v = [&](int c) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = c * kC + 4 * g + r;
+                v[r] = buf_load(rv, (t < T && i < N) ? (uint32_t)(t * HN + i) * 4u : kBufferOob);
+            }
+        };
+        if (n_chunks > 0) load_v(0);
+        wait_vmem();
+        for (int it = -4; it < n_chunks; ++it) {
+            if (it >= 0) {
+                const int c = it;
+                const float *sA = ringA + (c & 3) * Ly::kSlotA;
+                const float *sG = ringG + (c % 3) * Ly::kSlotG;
+                const float *sT = ringT + (c & 1) * Ly::kSlotT;
+                floatx4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int jb = 0; jb < NB; ++jb) {
+                    const floatx4 a4 = ld4(sA + Ly::oAs + li * SA + 16 * jb + 4 * g);
+                    const floatx4 r4 = ld4(sA + Ly::oRs + li * SA + 16 * jb + 4 * g);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        X = mfma(a4[r], S[jb][r], X);
+                        Y = mfma(r4[r], S[jb][r], Y);
+                    }
+                }
+                const floatx4 p4 = ld4(sG + Ly::oP + li * kST + 4 * g);
+                const floatx4 qk4 = ld4(sG + Ly::oQk + li * kST + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    X = mfma(p4[r], v[r], X);
+                    Y = mfma(qk4[r], v[r], Y);
+                }
+                const floatx4 ti4 = ld4(sT + li * kST + 4 * g);
+                floatx4 U = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) U = mfma(ti4[r], X[r], U);
+                const floatx4 qb4 = ld4(sG + Ly::oQb + li * kST + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) Y = mfma(qb4[r], U[r], Y);
+                // S^T <- diag(g_15) (S^T + B^^T U + K^^T V)
+#pragma unroll
+                for (int jb = 0; jb < NB; ++jb) {
+                    const floatx4 gl4 = ld4(sA + Ly::oGl + 16 * jb + 4 * g);
+                    const floatx4 bh4 = ld4(sA + Ly::oBhT + (16 * jb + li) * kST + 4 * g);
+                    const floatx4 kh4 = ld4(sA + Ly::oKhT + (16 * jb + li) * kST + 4 * g);
+                    floatx4 acc = S[jb];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc = mfma(bh4[r], U[r], acc);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc = mfma(kh4[r], v[r], acc);
+                    S[jb] = acc * gl4;
+                }
+                if (c + 1 < n_chunks) load_v(c + 1);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = c * kC + 4 * g + r;
+                    buf_store(Y[r], ry, (t < T && i < N) ? (uint32_t)(t * HN + i) * 4u : kBufferOob);
+                }
+            }
+            lds_barrier();
+        }
+        if (p.state_out) {
+            const auto rs = make_rsrc(p.state_out + state_off, (uint32_t)(N * N * 4));
+#pragma unroll
+            for (int jb = 0; jb < NB; ++jb) {
+                const int j0 = 16 * jb + 4 * g;
+                buf_store4(S[jb], rs, (i < N && j0 < N) ? (uint32_t)(i * N + j0) * 4u : kBufferOob);
+            }
+        }
+    } else if (role >= kRoleA) {
+        // ------------------------------------------------------------- stage A
+        // NB waves, 16 columns each; lane = (token quarter qg, column): tokens
+        // 4 qg .. 4 qg + 3 of column j.  Decay products run sequentially over
+        // the 4 tokens; quarters are chained by a 2-step scan over lane groups.
+        const int qg = lane >> 4;
+        const int j = (role - kRoleA) * 16 + li;
+        const bool col_ok = j < N;
+        const uint32_t voff = col_ok ? (uint32_t)((4 * qg * HN + j) * 4) : kBufferOob;
+        constexpr int kIn = PREP ? 4 : 5;  // r, w, k, a(lpha) [, b]
+        const float *src[5] = {p.r, p.w, p.k, p.a, PREP ? p.a : p.b};
+        __amdgpu_buffer_rsrc_t rs[kIn];
+#pragma unroll
+        for (int x = 0; x < kIn; ++x) rs[x] = make_rsrc(src[x] + tok_base, tok_bytes);
+        float kk_w = 0.0f, ka_w = 0.0f;
+        if constexpr (PREP) {
+            kk_w = col_ok ? p.k_k[h * N + j] : 0.0f;
+            ka_w = col_ok ? p.k_a[h * N + j] : 0.0f;
+        }
+        float raw[kIn][4];
+        auto load_chunk = [&](int c) {
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const int soff = c * chunk_bytes + tt * HN * 4;
+#pragma unroll
+                for (int x = 0; x < kIn; ++x)
+                    raw[x][tt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs[x], voff, soff, 0));
+            }
+        };
+        if (n_chunks > 0) load_chunk(0);
+        const int rowbase = 4 * qg * SA + j;  // LDS [token][column] index of (4 qg, j)
+        for (int it = -4; it < n_chunks; ++it) {
+            const int c = it + 3;
+            if (c >= 0 && c < n_chunks) {
+                wait_vmem();
+                const int nt = min(kC, T - c * kC);
+                float *sA = ringA + (c & 3) * Ly::kSlotA;
+                float *sH = ringH + (c & 1) * Ly::kSlotH;
+                float av[4], bv[4], kv[4], rv[4], dv[4];
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) {
+                    rv[tt] = raw[0][tt];
+                    // d = exp(-e^{-0.5} sigmoid(w)) = exp2(-e^{-0.5} log2(e) sigmoid(w)); padded tokens keep g.
+                    const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-raw[1][tt]));
+                    const float d = __builtin_amdgcn_exp2f(-0.8750387749f * sig);
+                    dv[tt] = nt == kC || 4 * qg + tt < nt ? d : 1.0f;
+                }
+                if constexpr (PREP) {
+                    const float *inv = ringN + (c & 1) * Ly::kSlotN + 4 * qg;
+#pragma unroll
+                    for (int tt = 0; tt < 4; ++tt) {
+                        const float alpha = raw[3][tt];
+                        const float kap = raw[2][tt] * kk_w * inv[tt];
+                        av[tt] = -kap;
+                        bv[tt] = kap * alpha;
+                        kv[tt] = raw[2][tt] * (1.0f + (alpha - 1.0f) * ka_w);
+                    }
+                } else {
+#pragma unroll
+                    for (int tt = 0; tt < 4; ++tt) {
+                        av[tt] = raw[3][tt];
+                        bv[tt] = raw[4][tt];
+                        kv[tt] = raw[2][tt];
+                    }
+                }
+                float gl[4];
+                {
+                    float gacc = 1.0f;
+#pragma unroll
+                    for (int tt = 0; tt < 4; ++tt) {
+                        gacc *= dv[tt];
+                        gl[tt] = gacc;
+                    }
+                }
+                // Inclusive scan of the quarter end products over the four lane
+                // groups, then shift by one group: base = product of d over the
+                // earlier quarters.  (Cross-lane reads run on every lane, outside
+                // any condition.)
+                float s1 = gl[3];
+                const float x1 = lane_from(s1, lane - 16);
+                s1 = qg >= 1 ? s1 * x1 : s1;
+                const float x2 = lane_from(s1, lane - 32);
+                s1 = qg >= 2 ? s1 * x2 : s1;
+                const float prev = lane_from(s1, lane - 16);
+                const float base = qg >= 1 ? prev : 1.0f;
+                float bh[4], kh[4];
+                float *pAs = sA + Ly::oAs + rowbase, *pRs = sA + Ly::oRs + rowbase;
+                float *pBh = sH + Ly::oBh + rowbase, *pKh = sH + Ly::oKh + rowbase;
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) {
+                    const float gprev = tt == 0 ? base : base * gl[tt - 1];
+                    const float gam = base * gl[tt];
+                    const float ig = __builtin_amdgcn_rcpf(gam);
+                    bh[tt] = bv[tt] * ig;
+                    kh[tt] = kv[tt] * ig;
+                    pAs[tt * SA] = av[tt] * gprev;
+                    pRs[tt * SA] = rv[tt] * gam;
+                    pBh[tt * SA] = bh[tt];
+                    pKh[tt * SA] = kh[tt];
+                }
+                *reinterpret_cast<floatx4 *>(sA + Ly::oBhT + j * kST + 4 * qg) = floatx4{bh[0], bh[1], bh[2], bh[3]};
+                *reinterpret_cast<floatx4 *>(sA + Ly::oKhT + j * kST + 4 * qg) = floatx4{kh[0], kh[1], kh[2], kh[3]};
+                if (qg == 3) sA[Ly::oGl + j] = base * gl[3];
+                // Next chunk's loads go out after the last use of this one's registers.
+                if (c + 1 < n_chunks) load_chunk(c + 1);
+            }
+            lds_barrier();
+        }
+    } else if (role == kRoleB1) {
+        // ------------------------------------------------------------ stage B1
+        for (int it = -4; it < n_chunks; ++it) {
+            const int c = it + 2;
+            if (c >= 0 && c < n_chunks) {
+                const float *sA = ringA + (c & 3) * Ly::kSlotA;
+                const float *sH = ringH + (c & 1) * Ly::kSlotH;
+                float *sG = ringG + (c % 3) * Ly::kSlotG;
+                floatx4 gab = {0.f, 0.f, 0.f, 0.f}, gp = gab, gqb = gab, gqk = gab;
+#pragma unroll
+                for (int jb = 0; jb < NB; ++jb) {
+                    const int o = li * SA + 16 * jb + 4 * g;
+                    const floatx4 a4 = ld4(sA + Ly::oAs + o), r4 = ld4(sA + Ly::oRs + o);
+                    const floatx4 b4 = ld4(sH + Ly::oBh + o), k4 = ld4(sH + Ly::oKh + o);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        gab = mfma(a4[r], b4[r], gab);
+                        gp = mfma(a4[r], k4[r], gp);
+                        gqb = mfma(r4[r], b4[r], gqb);
+                        gqk = mfma(r4[r], k4[r], gqk);
+                    }
+                }
+                // Register r: row t = 4 g + r, column s = li.
+                floatx4 gt;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int t = 4 * g + r, o = t * kST + li;
+                    gt[r] = li < t ? gab[r] : 0.0f;
+                    sG[Ly::oP + o] = li < t ? gp[r] : 0.0f;
+                    sG[Ly::oQb + o] = li <= t ? gqb[r] : 0.0f;
+                    sG[Ly::oQk + o] = li <= t ? gqk[r] : 0.0f;
+                }
+                *reinterpret_cast<floatx4 *>(sG + Ly::oGabT + li * kST + 4 * g) = gt;  // Gab^T[s = li][t]
+            }
+            lds_barrier();
+        }
+    } else {
+        // ------------------------------------------------------------ stage B2
+        // (model path) per-token inverse key norms one chunk ahead of stage A:
+        // lane = (token li, column group g + 4 m), partial sums folded over the
+        // four lane groups.
+        __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + tok_base, tok_bytes);
+        floatx4 kkw[NB], kraw[NB];
+        if constexpr (PREP) {
+#pragma unroll
+            for (int m = 0; m < NB; ++m) {
+                const int j0 = 4 * (g + 4 * m);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kkw[m][e] = j0 < N ? p.k_k[h * N + j0 + e] : 0.0f;
+            }
+        }
+        auto load_k = [&](int c) {
+#pragma unroll
+            for (int m = 0; m < NB; ++m) {
+                const int j0 = 4 * (g + 4 * m);
+                const uint32_t off = j0 < N ? (uint32_t)((li * HN + j0) * 4) : kBufferOob;
+                kraw[m] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, c * chunk_bytes, 0));
+            }
+        };
+        if (PREP && n_chunks > 0) load_k(0);
+        for (int it = -4; it < n_chunks; ++it) {
+            if constexpr (PREP) {
+                const int cn = it + 4;
+                if (cn < n_chunks) {
+                    wait_vmem();
+                    float sq = 0.0f;
+#pragma unroll
+                    for (int m = 0; m < NB; ++m)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float x = kraw[m][e] * kkw[m][e];
+                            sq = fmaf(x, x, sq);
+                        }
+                    if (cn + 1 < n_chunks) load_k(cn + 1);
+                    sq += lane_from(sq, lane ^ 16);
+                    sq += lane_from(sq, lane ^ 32);
+                    if (lane < kC) ringN[(cn & 1) * Ly::kSlotN + lane] = 1.0f / fmaxf(sqrtf(sq), 1e-12f);
+                }
+            }
+            const int c = it + 1;
+            if (c >= 0 && c < n_chunks) {
+                const float *GT = ringG + (c % 3) * Ly::kSlotG + Ly::oGabT;
+                float *sT = ringT + (c & 1) * Ly::kSlotT;
+                // Column `lane` (< 16) of (I - Gab)^{-1}, right-looking: once x_s is
+                // final, x_t += Gab[t][s] x_s for every t > s.
+                float x[kC];
+#pragma unroll
+                for (int t = 0; t < kC; ++t) x[t] = lane == t ? 1.0f : 0.0f;
+#pragma unroll
+                for (int s = 0; s < kC - 1; ++s) {
+                    float col[kC];
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        const floatx4 c4 = ld4(GT + s * kST + 4 * m);
+                        col[4 * m] = c4[0]; col[4 * m + 1] = c4[1]; col[4 * m + 2] = c4[2]; col[4 * m + 3] = c4[3];
+                    }
+#pragma unroll
+                    for (int t = s + 1; t < kC; ++t) x[t] = fmaf(col[t], x[s], x[t]);
+                }
+                if (lane < kC) {
+#pragma unroll
+                    for (int t = 0; t < kC; ++t) sT[t * kST + lane] = x[t];
+                }
+            }
+            lds_barrier();
+        }
+    }
+}
+
+template <int NB>
+hipError_t launch_nb(const WkvParams &p, int N, bool prep, hipStream_t stream) {
+    const int heads = p.B * p.H;
+    const int per_xcd = (heads + kXcds - 1) / kXcds;
+    const dim3 grid(per_xcd * kXcds), block(Roles<NB>::kWaves * kWave);
+    if (prep)
+        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, true>), grid, block, 0, stream, p, N, heads, per_xcd);
+    else
+        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, false>), grid, block, 0, stream, p, N, heads, per_xcd);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool wkv7_chunk_supported(int N) { return N >= 4 && N <= 64 && N % 4 == 0; }
+
+hipError_t launch_wkv7_chunked(const WkvParams &p, int N, bool prep, hipStream_t stream) {
+    if (p.B <= 0 || p.H <= 0) return hipSuccess;
+    if (!wkv7_chunk_supported(N)) return hipErrorInvalidValue;
+    switch ((N + 15) / 16) {
+        case 1: return launch_nb<1>(p, N, prep, stream);
+        case 2: return launch_nb<2>(p, N, prep, stream);
+        case 3: return launch_nb<3>(p, N, prep, stream);
+        default: return launch_nb<4>(p, N, prep, stream);
+    }
+}
+
+}  // namespace yuf
