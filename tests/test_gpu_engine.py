@@ -130,14 +130,16 @@ def test_tiny_model_prompt_and_greedy_match_reference(golden_dir, tmp_path):
         np.testing.assert_allclose(last, z["greedy_logits"][i], rtol=0, atol=LOGIT_ATOL)
 
 
-def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path):
+@pytest.mark.parametrize("steps", [80, 160])
+def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path, steps):
     """The 0.1B architecture (14L, d=640, 16x40, ROSA 128, V=20480) on a short
-    batch, prefill then decode, against the float64 oracle."""
+    batch, prefill then decode, against the float64 oracle.  2 x 160 tokens
+    put every prefill product on the 256-row GEMM tiles."""
     cfg = PRESETS["0.1b"]
     weights = synth_weights(cfg, seed=0)
     path = tmp_path / "m.yuf"
     write_yuf(path, cfg, weights)
-    tokens = prompt_tokens(1, 2, 80, cfg.vocab_size)
+    tokens = prompt_tokens(1, 2, steps, cfg.vocab_size)
     eng = Engine(Checkpoint.load(path), max_streams=2, max_tokens=256)
     got = eng.prefill(tokens, logits="all")
     oracle = OracleModel(cfg.to_dict(), weights)

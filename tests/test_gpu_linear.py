@@ -24,7 +24,11 @@ def run_linear(a, w, bias=None, act=0, residual=None):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 640, 640), (64, 640, 640), (300, 200, 12), (129, 130, 33),
-                                   (16384, 64, 640), (256, 2560, 640), (77, 20480, 640), (200, 640, 2560)])
+                                   (16384, 64, 640), (256, 2560, 640), (77, 20480, 640), (200, 640, 2560),
+                                   # 256-row tile path (N % 256 == 0 or N % 160 == 0, M >= 256), with
+                                   # row tails and K tails
+                                   (300, 640, 100), (512, 512, 36), (1000, 160, 640), (700, 1280, 64),
+                                   (2048, 640, 2560)])
 def test_linear_matches_float64(m, n, k):
     print(f"linear {m}x{n}x{k}", flush=True)
     rng = np.random.default_rng(m + n + k)
@@ -36,12 +40,13 @@ def test_linear_matches_float64(m, n, k):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2])
-def test_linear_epilogues(act):
+@pytest.mark.parametrize("m,n", [(150, 70), (384, 320), (260, 512)])
+def test_linear_epilogues(act, m, n):
     rng = np.random.default_rng(act)
-    a = rng.standard_normal((150, 96)).astype(np.float32)
-    w = (rng.standard_normal((70, 96)) * 0.1).astype(np.float32)
-    bias = rng.standard_normal(70).astype(np.float32)
-    res = rng.standard_normal((150, 70)).astype(np.float32)
+    a = rng.standard_normal((m, 96)).astype(np.float32)
+    w = (rng.standard_normal((n, 96)) * 0.1).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
     z = a.astype(np.float64) @ w.astype(np.float64).T + bias
     z = {0: z, 1: np.tanh(z), 2: 1.0 / (1.0 + np.exp(-z))}[act] + res
     np.testing.assert_allclose(run_linear(a, w, bias, act, res), z, rtol=1e-5, atol=1e-5)

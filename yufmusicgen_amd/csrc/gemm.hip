@@ -191,6 +191,156 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmGroup g, int per
 }
 
 // ---------------------------------------------------------------------------
+// Large-tile path for the prefill shapes (M a multiple of 256 in practice):
+// 512 threads = 8 waves in a 4 x 2 arrangement over a 256 x BN block tile
+// (BN = 256 for N % 256 == 0, BN = 160 for the d_model = 640 outputs), K tile
+// 16, double-buffered LDS, one workgroup per CU.  The tile sizes make the tile
+// count a multiple of the 256 CUs for every prefill product of the 0.1B model
+// (N = 640: 64 x 4 tiles; N = 5120: 64 x 20; N = 20480: 64 x 80), so no CU
+// idles through a partial last wave of tiles.  Each wave owns 64 x BN/2 as
+// 16 x 16 tiles of v_mfma_f32_16x16x4f32; for 4 consecutive k-steps a lane
+// reads its 4 k values of a row with one ds_read_b128 (k-step r uses k = 4 g + r
+// for lane group g on both operands).
+// ---------------------------------------------------------------------------
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+constexpr int kBigBM = 256, kBigBK = 16, kBigLd = kBigBK + 4, kBigThreads = 512;
+
+template <int ROWS>
+struct BigLoad {
+    static constexpr int kF4 = ROWS * (kBigBK / 4);                    // float4 per tile
+    static constexpr int kPer = (kF4 + kBigThreads - 1) / kBigThreads;  // per thread
+    float4 v[kPer];
+};
+
+template <int ROWS>
+__device__ __forceinline__ void big_load(BigLoad<ROWS> &t, __amdgpu_buffer_rsrc_t rsrc, int ld, int k0, int K,
+                                         int tid) {
+#pragma unroll
+    for (int i = 0; i < BigLoad<ROWS>::kPer; ++i) {
+        const int q = tid + i * kBigThreads;
+        const int row = q >> 2, k = k0 + (q & 3) * 4;
+        // K % 4 == 0 on this path: a float4 is wholly inside or outside [0, K).
+        const uint32_t off = (q < BigLoad<ROWS>::kF4 && k < K) ? (uint32_t)((size_t)row * ld + k) * 4u : kBufferOob;
+        t.v[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    }
+}
+
+template <int ROWS>
+__device__ __forceinline__ void big_store(const BigLoad<ROWS> &t, float *lds, int tid) {
+#pragma unroll
+    for (int i = 0; i < BigLoad<ROWS>::kPer; ++i) {
+        const int q = tid + i * kBigThreads;
+        if (q < BigLoad<ROWS>::kF4) *reinterpret_cast<float4 *>(lds + (q >> 2) * kBigLd + (q & 3) * 4) = t.v[i];
+    }
+}
+
+template <int BN>
+__global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int per_xcd) {
+    constexpr int WN = BN / 2, NT = WN / 16;
+    __shared__ __attribute__((aligned(16))) float As[2][kBigBM * kBigLd];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BN * kBigLd];
+
+    const GemmParams &p = g.p[blockIdx.y];
+    const int tiles_n = g.tiles_n[blockIdx.y];
+    const int flat = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (flat >= g.total[blockIdx.y]) return;
+    const int bm = flat / tiles_n, bn = flat - bm * tiles_n;
+    const int m0 = bm * kBigBM, n0 = bn * BN;
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g4 = lane >> 4, li = lane & 15;
+    const int rows_a = min(kBigBM, p.M - m0), rows_w = min(BN, p.N - n0);
+    const auto ra = make_rsrc(p.A + (size_t)m0 * p.lda, (uint32_t)(((size_t)(rows_a - 1) * p.lda + p.K) * 4));
+    const auto rw = make_rsrc(p.W + (size_t)n0 * p.ldw, (uint32_t)(((size_t)(rows_w - 1) * p.ldw + p.K) * 4));
+
+    floatx4 acc[4][NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int k_tiles = (p.K + kBigBK - 1) / kBigBK;
+    BigLoad<kBigBM> ta;
+    BigLoad<BN> tb;
+    big_load(ta, ra, p.lda, 0, p.K, tid);
+    big_load(tb, rw, p.ldw, 0, p.K, tid);
+    big_store(ta, As[0], tid);
+    big_store(tb, Bs[0], tid);
+    lds_barrier();
+
+    for (int kt = 0; kt < k_tiles; ++kt) {
+        const int cur = kt & 1;
+        const bool more = kt + 1 < k_tiles;
+        if (more) {
+            big_load(ta, ra, p.lda, (kt + 1) * kBigBK, p.K, tid);
+            big_load(tb, rw, p.ldw, (kt + 1) * kBigBK, p.K, tid);
+        }
+        floatx4 af[4], bf[NT];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            af[i] = *reinterpret_cast<const floatx4 *>(As[cur] + (wm * 64 + i * 16 + li) * kBigLd + 4 * g4);
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+            bf[j] = *reinterpret_cast<const floatx4 *>(Bs[cur] + (wn * WN + j * 16 + li) * kBigLd + 4 * g4);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][r], bf[j][r], acc[i][j], 0, 0, 0);
+        if (more) {
+            big_store(ta, As[cur ^ 1], tid);
+            big_store(tb, Bs[cur ^ 1], tid);
+        }
+        lds_barrier();
+    }
+
+    // Accumulator register r of lane l: row 4 (l / 16) + r, column l % 16 of its 16 x 16 tile.
+    if constexpr (BN % 128 == 0) {
+        if (p.silu_pair) {
+            // Each wave's columns are whole 64-row blocks [32 "in" | 32 "gate"].
+#pragma unroll
+            for (int b = 0; b < WN / 64; ++b)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int hcol = (n0 + wn * WN + 64 * b) / 2 + 16 * h + li;
+                    if (hcol >= p.N / 2) continue;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
+                            if (row < p.M) {
+                                const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
+                                p.C[(size_t)row * p.ldc + hcol] = x / (1.0f + expf(-x)) * gt;
+                            }
+                        }
+                }
+            return;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int col = n0 + wn * WN + j * 16 + li;
+        if (col >= p.N) continue;
+        const float bias = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
+                if (row < p.M) {
+                    float x = apply_act(acc[i][j][r] + bias, p.act);
+                    if (p.residual) x += p.residual[(size_t)row * p.ldr + col];
+                    p.C[(size_t)row * p.ldc + col] = x;
+                }
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Short-M path (decode: M <= 64 rows, one token per stream).  The product is
 // bound by streaming W from HBM, so parallelism comes from N and K instead of
 // M: each wave owns 64 rows x 64 columns (2 x 2 MFMA 32x32 tiles) over a K
@@ -402,6 +552,30 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
         ++n;
     }
     if (n == 0) return hipSuccess;
+    // Large-tile path when every product of the group fits one of its tile widths.
+    bool fit256 = true, fit160 = true;
+    for (int i = 0; i < n; ++i) {
+        const GemmParams &p = g.p[i];
+        const bool big_ok = p.M >= kBigBM && p.K % 4 == 0 &&
+                            (size_t)kBigBM * p.lda * 4 < (1u << 31) && (size_t)256 * p.ldw * 4 < (1u << 31);
+        fit256 = fit256 && big_ok && p.N % 256 == 0;
+        fit160 = fit160 && big_ok && p.N % 160 == 0 && !p.silu_pair;
+    }
+    if (fit256 || fit160) {
+        const int bn = fit256 ? 256 : 160;
+        int big_max = 0;
+        for (int i = 0; i < n; ++i) {
+            g.tiles_n[i] = g.p[i].N / bn;
+            g.total[i] = ((g.p[i].M + kBigBM - 1) / kBigBM) * g.tiles_n[i];
+            big_max = std::max(big_max, g.total[i]);
+        }
+        const int per_xcd = (big_max + kXcds - 1) / kXcds;
+        if (fit256)
+            hipLaunchKernelGGL(gemm_big_kernel<256>, dim3(per_xcd * kXcds, n), dim3(kBigThreads), 0, stream, g, per_xcd);
+        else
+            hipLaunchKernelGGL(gemm_big_kernel<160>, dim3(per_xcd * kXcds, n), dim3(kBigThreads), 0, stream, g, per_xcd);
+        return hipGetLastError();
+    }
     const int per_xcd = (max_total + kXcds - 1) / kXcds;
     hipLaunchKernelGGL(gemm_f32_kernel, dim3(per_xcd * kXcds, n), dim3(kThreads), 0, stream, g, per_xcd);
     return hipGetLastError();

@@ -215,16 +215,25 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
                     part[lane * ZS + tau] = acc;
                 }
                 wave_lds_sync();
+                // Sums over the 64 lanes' partials and the Toeplitz products use
+                // independent accumulators: these chains are the scan's critical path.
                 if (lane <= C) {
-                    double acc = 0.0;
-                    for (int k = 0; k < kWave; ++k) acc += part[k * ZS + lane];
-                    fv[lane] = acc;
+                    double a8[8] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                    for (int k = 0; k < kWave; k += 8)
+#pragma unroll
+                        for (int m = 0; m < 8; ++m) a8[m] += part[(k + m) * ZS + lane];
+                    fv[lane] = ((a8[0] + a8[1]) + (a8[2] + a8[3])) + ((a8[4] + a8[5]) + (a8[6] + a8[7]));
                 }
                 wave_lds_sync();
                 if (lane <= C) {
-                    double acc = 0.0;
-                    for (int sg = 0; sg <= lane; ++sg) acc = fma(ell[lane - sg], fv[sg], acc);
-                    pv[s][lane] = (float)acc;
+                    double a4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+                    for (int sg = 0; sg <= C; ++sg) {
+                        const double coef = sg <= lane ? ell[sg <= lane ? lane - sg : 0] : 0.0;
+                        a4[sg & 3] = fma(coef, fv[sg], a4[sg & 3]);
+                    }
+                    pv[s][lane] = (float)((a4[0] + a4[1]) + (a4[2] + a4[3]));
                 }
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) m0b[s][lane + e * kWave] = m0[e];
