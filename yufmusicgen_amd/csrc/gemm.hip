@@ -193,7 +193,8 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmGroup g, int per
 // ---------------------------------------------------------------------------
 // Large-tile path for the prefill shapes (M a multiple of 256 in practice):
 // 512 threads = 8 waves in a 4 x 2 arrangement over a 256 x BN block tile
-// (BN = 256 for N % 256 == 0, BN = 160 for the d_model = 640 outputs), K tile
+// (BN = 256 for N % 256 == 0, BN = 160 for the d_model = 640 outputs, 128 and
+// 64 for the narrow ROSA input and low-rank products), K tile
 // 16, double-buffered LDS, one workgroup per CU.  The tile sizes make the tile
 // count a multiple of the 256 CUs for every prefill product of the 0.1B model
 // (N = 640: 64 x 4 tiles; N = 5120: 64 x 20; N = 20480: 64 x 80), so no CU
@@ -234,11 +235,21 @@ __device__ __forceinline__ void big_store(const BigLoad<ROWS> &t, float *lds, in
     }
 }
 
-template <int BN>
+// Epilogue of the large-tile path through LDS: 16 accumulator rows of a wave at
+// a time are written to LDS and read back row-contiguous, so every global
+// access (C, residual, bias) is a 16-byte run along a row.  Needs 16-byte
+// aligned C / residual / bias and row strides that are multiples of 4 floats.
+template <int WN>
+__device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4) {
+    return *reinterpret_cast<const float4 *>(stage + row * (WN + 4) + 4 * c4);
+}
+
+template <int BN, bool STAGED>
 __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int per_xcd) {
     constexpr int WN = BN / 2, NT = WN / 16;
-    __shared__ __attribute__((aligned(16))) float As[2][kBigBM * kBigLd];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BN * kBigLd];
+    __shared__ __attribute__((aligned(16))) float lds[2 * (kBigBM + BN) * kBigLd];
+    float(*As)[kBigBM * kBigLd] = reinterpret_cast<float(*)[kBigBM * kBigLd]>(lds);
+    float(*Bs)[BN * kBigLd] = reinterpret_cast<float(*)[BN * kBigLd]>(lds + 2 * kBigBM * kBigLd);
 
     const GemmParams &p = g.p[blockIdx.y];
     const int tiles_n = g.tiles_n[blockIdx.y];
@@ -298,6 +309,75 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
     }
 
     // Accumulator register r of lane l: row 4 (l / 16) + r, column l % 16 of its 16 x 16 tile.
+    if constexpr (STAGED) {
+        // The K loop ended with a barrier: LDS is free.  Wave-private staging areas.
+        constexpr int SW = WN + 4;
+        float *stage = lds + wave * 16 * SW;
+        const int row0 = m0 + wm * 64;
+        if (p.silu_pair) {
+            if constexpr (BN % 128 == 0) {
+                constexpr int HW = WN / 2;  // output columns of the wave
+                const int hcol0 = (n0 + wn * WN) / 2;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int b = 0; b < WN / 64; ++b)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
+                                stage[(4 * g4 + r) * SW + 32 * b + 16 * h + li] = x / (1.0f + expf(-x)) * gt;
+                            }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+                    for (int t = 0; t < 16 * HW / 4 / 64; ++t) {
+                        const int q = lane + 64 * t, row = q / (HW / 4), c4 = q % (HW / 4);
+                        const int grow = row0 + i * 16 + row;
+                        if (grow < p.M)
+                            *reinterpret_cast<float4 *>(p.C + (size_t)grow * p.ldc + hcol0 + 4 * c4) =
+                                stage_read<WN>(stage, row, c4);
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                }
+            }
+            return;
+        }
+        const int col0 = n0 + wn * WN;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < NT; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) stage[(4 * g4 + r) * SW + 16 * j + li] = acc[i][j][r];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+            for (int t = 0; t < 16 * WN / 4 / 64; ++t) {
+                const int q = lane + 64 * t, row = q / (WN / 4), c4 = q % (WN / 4);
+                const int grow = row0 + i * 16 + row, col = col0 + 4 * c4;
+                if (grow < p.M) {
+                    float4 x = stage_read<WN>(stage, row, c4);
+                    if (p.bias) {
+                        const float4 b4 = *reinterpret_cast<const float4 *>(p.bias + col);
+                        x.x += b4.x; x.y += b4.y; x.z += b4.z; x.w += b4.w;
+                    }
+                    x.x = apply_act(x.x, p.act); x.y = apply_act(x.y, p.act);
+                    x.z = apply_act(x.z, p.act); x.w = apply_act(x.w, p.act);
+                    if (p.residual) {
+                        const float4 r4 = *reinterpret_cast<const float4 *>(p.residual + (size_t)grow * p.ldr + col);
+                        x.x += r4.x; x.y += r4.y; x.z += r4.z; x.w += r4.w;
+                    }
+                    *reinterpret_cast<float4 *>(p.C + (size_t)grow * p.ldc + col) = x;
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        }
+        return;
+    }
     if constexpr (BN % 128 == 0) {
         if (p.silu_pair) {
             // Each wave's columns are whole 64-row blocks [32 "in" | 32 "gate"].
@@ -496,6 +576,14 @@ __global__ void gemm_splitk_reduce_kernel(GemmParams p, int splits) {
     }
 }
 
+template <int BN>
+void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStream_t stream) {
+    if (staged)
+        hipLaunchKernelGGL((gemm_big_kernel<BN, true>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+    else
+        hipLaunchKernelGGL((gemm_big_kernel<BN, false>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+}
+
 int skinny_splits(int N, int K) {
     const int wave_tiles = (N + 63) / 64;
     const int max_splits = (K + 31) / 32;
@@ -553,16 +641,18 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
     }
     if (n == 0) return hipSuccess;
     // Large-tile path when every product of the group fits one of its tile widths.
-    bool fit256 = true, fit160 = true;
+    bool fit256 = true, fit160 = true, fit128 = true, fit64 = true;
     for (int i = 0; i < n; ++i) {
         const GemmParams &p = g.p[i];
         const bool big_ok = p.M >= kBigBM && p.K % 4 == 0 &&
                             (size_t)kBigBM * p.lda * 4 < (1u << 31) && (size_t)256 * p.ldw * 4 < (1u << 31);
         fit256 = fit256 && big_ok && p.N % 256 == 0;
         fit160 = fit160 && big_ok && p.N % 160 == 0 && !p.silu_pair;
+        fit128 = fit128 && big_ok && p.N % 128 == 0;
+        fit64 = fit64 && big_ok && p.N % 64 == 0 && !p.silu_pair;
     }
-    if (fit256 || fit160) {
-        const int bn = fit256 ? 256 : 160;
+    if (fit256 || fit160 || fit128 || fit64) {
+        const int bn = fit256 ? 256 : fit160 ? 160 : fit128 ? 128 : 64;
         int big_max = 0;
         for (int i = 0; i < n; ++i) {
             g.tiles_n[i] = g.p[i].N / bn;
@@ -570,10 +660,20 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
             big_max = std::max(big_max, g.total[i]);
         }
         const int per_xcd = (big_max + kXcds - 1) / kXcds;
-        if (fit256)
-            hipLaunchKernelGGL(gemm_big_kernel<256>, dim3(per_xcd * kXcds, n), dim3(kBigThreads), 0, stream, g, per_xcd);
-        else
-            hipLaunchKernelGGL(gemm_big_kernel<160>, dim3(per_xcd * kXcds, n), dim3(kBigThreads), 0, stream, g, per_xcd);
+        bool staged = true;  // 16-byte epilogue accesses need aligned C / residual / bias rows
+        for (int i = 0; i < n; ++i) {
+            const GemmParams &p = g.p[i];
+            const uintptr_t bits = reinterpret_cast<uintptr_t>(p.C) | reinterpret_cast<uintptr_t>(p.residual) |
+                                   reinterpret_cast<uintptr_t>(p.bias);
+            staged = staged && (bits & 15) == 0 && p.ldc % 4 == 0 && (!p.residual || p.ldr % 4 == 0);
+        }
+        const dim3 grid(per_xcd * kXcds, n), block(kBigThreads);
+switch (bn) {
+            case 256: launch_big<256>(g, per_xcd, staged, grid, stream); break;
+            case 160: launch_big<160>(g, per_xcd, staged, grid, stream); break;
+            case 128: launch_big<128>(g, per_xcd, staged, grid, stream); break;
+            default: launch_big<64>(g, per_xcd, staged, grid, stream); break;
+        }
         return hipGetLastError();
     }
     const int per_xcd = (max_total + kXcds - 1) / kXcds;
