@@ -101,6 +101,22 @@ __global__ void fill_kernel(float *p, size_t n, float value) {
         p[i] = value;
 }
 
+// ROSA gates in place: row r of x holds [cand | write | read_raw] (D each, row
+// stride ld); cand becomes e = tanh(cand) sigmoid(write) and write becomes the
+// read gate sigmoid(read_raw) (yufmusicgen/model.py:303-311; the same float
+// expressions as the scan kernel's own activation path).
+__global__ void rosa_gates_kernel(float *x, int M, int D, int ld) {
+    const size_t n = (size_t)M * D;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i / D), c = (int)(i - (size_t)r * D);
+        float *row = x + (size_t)r * ld;
+        const float cv = row[c], wv = row[D + c], rv = row[2 * D + c];
+        const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * cv) + 1.0f);
+        row[c] = th * __frcp_rn(1.0f + __expf(-wv));
+        row[D + c] = __frcp_rn(1.0f + __expf(-rv));
+    }
+}
+
 int grid_for(size_t n, int block) {
     size_t g = (n + block - 1) / block;
     return (int)(g < 65536 ? (g > 0 ? g : 1) : 65536);
@@ -149,6 +165,13 @@ hipError_t launch_save_prev(const float *x, int Bn, int T, int d, float *prev_st
 hipError_t launch_gather_last(const float *x, int Bn, int T, int d, float *out, hipStream_t stream) {
     if (Bn <= 0 || T <= 0) return hipSuccess;
     hipLaunchKernelGGL(gather_last_kernel, dim3(Bn), dim3(256), 0, stream, x, Bn, T, d, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_rosa_gates(float *x, int M, int D, int ld, hipStream_t stream) {
+    const size_t n = (size_t)M * D;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(rosa_gates_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, x, M, D, ld);
     return hipGetLastError();
 }
 

@@ -293,9 +293,11 @@ int forward_pass(Engine &e, int n, int Tc, float *logits, int mode, int row_stri
         // ROSA
         ENG_TRY(launch_layernorm(e.h, M, d, w.ln_r_w, w.ln_r_b, nullptr, e.xn, st), "ln_rosa");
         if ((rc = gemm(e, M, 3 * D, d, e.xn, d, w.rosa_w3, d, e.rosa3, 3 * D, w.rosa_b3)) != YUF_OK) return rc;
+        // Gates on all M rows in parallel, so the sequential scan only loads e and the gate.
+        ENG_TRY(launch_rosa_gates(e.rosa3, M, D, 3 * D, st), "rosa_gates");
         RosaParams rp;
         rp.B = n; rp.T = Tc; rp.D = D; rp.ld = 3 * D;
-        rp.cand = e.rosa3; rp.write = e.rosa3 + D; rp.read_raw = e.rosa3 + 2 * D;
+        rp.e_pre = e.rosa3; rp.g_pre = e.rosa3 + D;
         rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
         rp.memory_in = ros; rp.memory_out = ros; rp.slot = e.slots_dev; rp.read_out = e.rread;
         ENG_TRY(launch_rosa(rp, st), "rosa");

@@ -44,6 +44,10 @@ struct RosaParams {
     float *memory_out = nullptr;
     const int *slot = nullptr;
     float *read_out = nullptr;  // [(b * T + t) * D + c]
+    // Prepared inputs (model path): e = sigmoid(write) tanh(cand) and the read
+    // gate sigmoid(read_raw), same indexing as the pre-activations; when set,
+    // cand / write / read_raw are ignored and the read is gated.
+    const float *e_pre = nullptr, *g_pre = nullptr;
 };
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream);
 
@@ -96,6 +100,8 @@ hipError_t launch_save_prev(const float *x, int Bn, int T, int d, float *prev_st
 hipError_t launch_gather_last(const float *x, int Bn, int T, int d, float *out, hipStream_t stream);
 // state blob pack/unpack and clearing.
 hipError_t launch_fill(float *p, size_t n, float value, hipStream_t stream);
+// In place on rows [cand | write | read_raw] of stride ld: cand <- e, write <- gate.
+hipError_t launch_rosa_gates(float *x, int M, int D, int ld, hipStream_t stream);
 
 // -------------------------------------------------------------------- sampling
 hipError_t launch_sample(int n, int V, const float *logits, float temperature, int top_k,

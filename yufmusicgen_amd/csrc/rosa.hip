@@ -18,10 +18,12 @@
 // So the only cross-channel reductions are the C+1 dot products f (one batch
 // per chunk), not one wave reduction per token as in the direct recurrence.
 //
-// One workgroup per stream, 1 consumer wave + 8 producer waves, three LDS
+// One workgroup per stream, 1 consumer wave + 6 producer waves, three LDS
 // stages in flight (chunk i+1 staged, chunk i solved, chunk i-1 emitted):
-//   producers, A(i+1): load chunk i+1's pre-activations (bounds-checked buffer
-//       loads), write e and the gate to LDS, run the per-channel z recurrence;
+//   producers, A(i+1): turn chunk i+1's pre-activations (loaded one iteration
+//       earlier with bounds-checked buffer loads) into e and the gate in LDS --
+//       or take e and the gate as computed by the model's input projection --
+//       and run the per-channel z recurrence;
 //   consumer, B(i):   f = u.(lambda^tau m_0 + z_tau) for tau = 0..C (per-lane
 //       partials, transposed through LDS), p = L f, then the chunk-end state;
 //   producers, O(i-1): per channel, m_tau = lambda (m_{tau-1} - 2 p_tau u) + e_tau
@@ -34,8 +36,11 @@ namespace yuf {
 namespace {
 
 constexpr int kWave = 64;
-constexpr int kProducerWaves = 8;
-constexpr int kThreads = (1 + kProducerWaves) * kWave;
+// Waves w and w + 4 of a workgroup share a SIMD: the consumer (wave 0) keeps its
+// SIMD to itself (wave 4 only joins the barriers), six producers take waves
+// 1-3 and 5-7.
+constexpr int kProducerWaves = 6;
+constexpr int kThreads = 8 * kWave;
 constexpr int kStages = 3;
 
 template <int EPL>
@@ -43,8 +48,9 @@ struct Cfg {
     static constexpr int C = EPL <= 2 ? 16 : (EPL == 4 ? 8 : (EPL == 8 ? 4 : 2));  // tokens per chunk
     static constexpr int DP = EPL * kWave;                                          // padded channels
     static constexpr int ZS = C + 1;          // odd row stride of the transposed z / partial arrays
-    static constexpr int CH = DP / kProducerWaves;  // channels per producer wave
-    static constexpr int CPL = CH > kWave ? CH / kWave : 1;  // channels per producer lane
+    static constexpr int CH = (DP + kProducerWaves - 1) / kProducerWaves;  // channels per producer wave
+    static constexpr int CPL = (CH + kWave - 1) / kWave;                   // channels per producer lane
+    static constexpr int kItems = (C * CH + kWave - 1) / kWave;            // (token, channel) loads per lane
 };
 
 // LDS-only ordering between lanes of one wave (no s_barrier).
@@ -73,36 +79,65 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int D = p.D;
     const int slot = p.slot ? p.slot[bb] : bb;
-    const bool gated = p.read_raw != nullptr;
+    const bool gated = p.read_raw != nullptr || p.e_pre != nullptr;
     const int n_chunks = (p.T + C - 1) / C;
 
     // ------------------------------------------------------------ producers
-    const int pw = wave - 1;
-    auto stage_in = [&](int ch) {  // A(ch)
-        const int s = ch % kStages, t0 = ch * C, nt = min(C, p.T - t0);
+    const int pw = wave < 4 ? wave - 1 : wave - 2;  // producer index on waves 1-3, 5-7
+    const bool producer = wave != 0 && wave != 4;
+    const bool prepared = p.e_pre != nullptr;
+    // Next chunk's inputs, loaded one iteration ahead: (cand, write, read_raw) or,
+    // prepared, (e, gate).
+    float in0[K::kItems], in1[K::kItems], in2[K::kItems];
+    auto load_in = [&](int ch) {
+        const int t0 = ch * C, nt = min(C, p.T - t0);
         const size_t base = (size_t)(bb * p.T + t0) * p.ld;
         const uint32_t bytes = (uint32_t)(((nt - 1) * p.ld + D) * 4);
-        const auto rc = make_rsrc(p.cand + base, bytes), rw = make_rsrc(p.write + base, bytes);
-        const auto rr = make_rsrc(gated ? p.read_raw + base : p.cand + base, gated ? bytes : 0u);
-        for (int q = lane; q < C * CH; q += kWave) {
+        const auto r0 = make_rsrc((prepared ? p.e_pre : p.cand) + base, bytes);
+        const auto r1 = make_rsrc((prepared ? p.g_pre : p.write) + base, bytes);
+        const auto r2 = make_rsrc(gated && !prepared ? p.read_raw + base : p.cand + base, gated && !prepared ? bytes : 0u);
+#pragma unroll
+        for (int it = 0; it < K::kItems; ++it) {
+            const int q = lane + it * kWave;
             const int tau = q / CH, c = pw * CH + (q - tau * CH);
-            const uint32_t off = (c < D && tau < nt) ? (uint32_t)(tau * p.ld + c) * 4u : kBufferOob;
-            const float cv = buf_load(rc, off), wv = buf_load(rw, off), rv = buf_load(rr, off);
-            // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).  Out-of-range
-            // tokens and channels read 0 and give e = 0.
-            const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * cv) + 1.0f);
-            ew[s][tau * DP + c] = th * __frcp_rn(1.0f + __expf(-wv));
-            gt[s][tau * DP + c] = gated ? __frcp_rn(1.0f + __expf(-rv)) : 1.0f;
+            const uint32_t off = (q < C * CH && c < D && tau < nt) ? (uint32_t)(tau * p.ld + c) * 4u : kBufferOob;
+            in0[it] = buf_load(r0, off);
+            in1[it] = buf_load(r1, off);
+            in2[it] = buf_load(r2, off);
+        }
+    };
+    auto stage_in = [&](int ch) {  // A(ch), from the registers load_in(ch) filled
+        const int s = ch % kStages;
+#pragma unroll
+        for (int it = 0; it < K::kItems; ++it) {
+            const int q = lane + it * kWave;
+            const int tau = q / CH, c = pw * CH + (q - tau * CH);
+            if (q < C * CH && c < DP) {
+                float e, gv;
+                if (prepared) {
+                    e = in0[it];
+                    gv = in1[it];
+                } else {
+                    // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).  Out-of-range
+                    // tokens and channels read 0 and give e = 0.
+                    const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * in0[it]) + 1.0f);
+                    e = th * __frcp_rn(1.0f + __expf(-in1[it]));
+                    gv = gated ? __frcp_rn(1.0f + __expf(-in2[it])) : 1.0f;
+                }
+                ew[s][tau * DP + c] = e;
+                gt[s][tau * DP + c] = gv;
+            }
         }
         wave_lds_sync();
 #pragma unroll
         for (int k = 0; k < CPL; ++k) {
             const int cc = lane + k * kWave;
-            if (cc < CH) {
-                const int c = pw * CH + cc;
+            const int c = pw * CH + cc;
+            if (cc < CH && c < DP) {
                 const float lam = lam_s[c];
                 float z = 0.0f;
                 zt[s][c * ZS] = 0.0f;
+#pragma unroll
                 for (int tau = 0; tau < C; ++tau) {
                     z = fmaf(lam, z, ew[s][tau * DP + c]);
                     zt[s][c * ZS + tau + 1] = z;
@@ -117,14 +152,17 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
 #pragma unroll
         for (int k = 0; k < CPL; ++k) {
             const int cc = lane + k * kWave;
-            if (cc < CH) {
-                const int c = pw * CH + cc;
+            const int c = pw * CH + cc;
+            if (cc < CH && c < DP) {
                 const float lam = lam_s[c], u = u_s[c];
                 float m = m0b[s][c];
-                for (int tau = 0; tau < nt; ++tau) {
+                // All C steps run (tokens past nt have e = 0 and are not stored), so
+                // the LDS reads are independent of the chain and issue up front.
+#pragma unroll
+                for (int tau = 0; tau < C; ++tau) {
                     m = fmaf(lam, fmaf(-2.0f * pv[s][tau], u, m), ew[s][tau * DP + c]);
                     const float rv = fmaf(-2.0f * pv[s][tau + 1], u, m) * gt[s][tau * DP + c];
-                    buf_store(rv, ro, c < D ? (uint32_t)(tau * D + c) * 4u : kBufferOob);
+                    buf_store(rv, ro, (c < D && tau < nt) ? (uint32_t)(tau * D + c) * 4u : kBufferOob);
                 }
             }
         }
@@ -193,7 +231,11 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
         wait_vmem();
     }
     lds_barrier();  // lam_s / u_s visible to the producers
-    if (wave > 0 && n_chunks > 0) stage_in(0);
+    if (producer && n_chunks > 0) {
+        load_in(0);
+        stage_in(0);
+        if (n_chunks > 1) load_in(1);
+    }
     lds_barrier();
 
     for (int i = 0; i <= n_chunks; ++i) {
@@ -243,21 +285,27 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
                 float acc[EPL], pwr[EPL];
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) { acc[e] = 0.0f; pwr[e] = m0[e]; }
-                for (int sg = 0; sg < nt; ++sg) {
+#pragma unroll
+                for (int sg = 0; sg < C; ++sg) {
                     const float ps = pv[s][sg];
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) {
-                        acc[e] = lam[e] * fmaf(ps, u[e], acc[e]);
-                        pwr[e] *= lam[e];
+                        if (sg < nt) {
+                            acc[e] = lam[e] * fmaf(ps, u[e], acc[e]);
+                            pwr[e] *= lam[e];
+                        }
                     }
                 }
 #pragma unroll
                 for (int e = 0; e < EPL; ++e)
                     m0[e] = fmaf(-2.0f, acc[e], pwr[e] + zt[s][(lane + e * kWave) * ZS + nt]);
             }
-        } else {
+        } else if (producer) {
             if (i >= 1) emit(i - 1);
-            if (i + 1 < n_chunks) stage_in(i + 1);
+            if (i + 1 < n_chunks) {
+                stage_in(i + 1);
+                if (i + 2 < n_chunks) load_in(i + 2);
+            }
         }
         lds_barrier();
     }
