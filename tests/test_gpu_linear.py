@@ -28,7 +28,9 @@ def run_linear(a, w, bias=None, act=0, residual=None):
                                    # 256-row tile path (N % 256 == 0 or N % 160 == 0, M >= 256), with
                                    # row tails and K tails
                                    (300, 640, 100), (512, 512, 36), (1000, 160, 640), (700, 1280, 64),
-                                   (2048, 640, 2560), (640, 384, 640), (512, 64, 640), (300, 192, 100)])
+                                   (2048, 640, 2560), (640, 384, 640), (512, 64, 640), (300, 192, 100),
+                                   # decode path (M <= 64): column tails, short K, long K
+                                   (64, 5120, 640), (37, 100, 36), (64, 640, 2560), (1, 20480, 640), (16, 64, 64)])
 def test_linear_matches_float64(m, n, k):
     print(f"linear {m}x{n}x{k}", flush=True)
     rng = np.random.default_rng(m + n + k)
@@ -40,7 +42,7 @@ def test_linear_matches_float64(m, n, k):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2])
-@pytest.mark.parametrize("m,n", [(150, 70), (384, 320), (260, 512), (300, 384), (257, 64)])
+@pytest.mark.parametrize("m,n", [(150, 70), (384, 320), (260, 512), (300, 384), (257, 64), (48, 70), (64, 640)])
 def test_linear_epilogues(act, m, n):
     rng = np.random.default_rng(act)
     a = rng.standard_normal((m, 96)).astype(np.float32)

@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <set>
@@ -72,8 +73,17 @@ struct Engine {
     // Device staging for the host-buffer entry points (grown on demand).
     DeviceBuf host_tokens, host_logits;
     size_t host_tokens_cap = 0, host_logits_cap = 0;
+    // Decode step captured as a HIP graph (~30 kernels per layer replayed with
+    // one launch); rebuilt when n or the token / logit buffers change.
+    // YUF_NO_GRAPH=1 runs every step eagerly.
+    bool use_graphs = true;
+    hipGraphExec_t step_exec = nullptr;
+    int step_n = 0;
+    const int32_t *step_tok = nullptr;
+    float *step_logits = nullptr;
 
     ~Engine() {
+        if (step_exec) (void)hipGraphExecDestroy(step_exec);
         if (stream) {
             (void)hipStreamSynchronize(stream);
             (void)hipStreamDestroy(stream);
@@ -372,6 +382,39 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
     return YUF_OK;
 }
 
+// One decode step (T = 1, last-position logits) of n streams whose slots are
+// already on the device, replayed from a captured graph when possible.  The
+// captured work is kernels and one device-to-device copy only (no memset
+// nodes, no host synchronisation).
+int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
+    if (!e.use_graphs) return prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
+    if (!(e.step_exec && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
+        if (e.step_exec) {
+            ENG_TRY(hipGraphExecDestroy(e.step_exec), "graph destroy");
+            e.step_exec = nullptr;
+        }
+        ENG_TRY(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal), "capture begin");
+        const int rc = prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
+        hipGraph_t graph = nullptr;
+        const hipError_t ce = hipStreamEndCapture(e.stream, &graph);
+        if (rc != YUF_OK || ce != hipSuccess) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return rc != YUF_OK ? rc : hip_fail(ce, "capture end");
+        }
+        const hipError_t ie = hipGraphInstantiate(&e.step_exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        if (ie != hipSuccess) {
+            e.step_exec = nullptr;
+            return hip_fail(ie, "graph instantiate");
+        }
+        e.step_n = n;
+        e.step_tok = tokens_dev;
+        e.step_logits = logits_dev;
+    }
+    ENG_TRY(hipGraphLaunch(e.step_exec, e.stream), "graph launch");
+    return YUF_OK;
+}
+
 }  // namespace
 
 }  // namespace yuf
@@ -398,6 +441,7 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
     if (!h) return fail(YUF_ERR_OOM, "host allocation failed");
     Engine &e = h->e;
     e.s = s;
+    if (const char *ng = std::getenv("YUF_NO_GRAPH")) e.use_graphs = std::strcmp(ng, "1") != 0;
     e.max_streams = max_streams;
     e.max_tokens = max_tokens;
 
@@ -553,9 +597,12 @@ extern "C" int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T, 
     ENG_TRY(hipMemcpyAsync(e.host_tokens.p, tokens, n_tok * sizeof(int), hipMemcpyHostToDevice, e.stream),
             "tokens upload");
     if ((rc = upload_slots(e, n, slots)) != YUF_OK) return rc;
-    if ((rc = prefill_impl(e, n, T, static_cast<int *>(e.host_tokens.p), static_cast<float *>(e.host_logits.p),
-                           logits_mode)) != YUF_OK)
-        return rc;
+    if (T == 1 && logits_mode == YUF_LOGITS_LAST)
+        rc = step_impl(e, n, static_cast<int *>(e.host_tokens.p), static_cast<float *>(e.host_logits.p));
+    else
+        rc = prefill_impl(e, n, T, static_cast<int *>(e.host_tokens.p), static_cast<float *>(e.host_logits.p),
+                          logits_mode);
+    if (rc != YUF_OK) return rc;
     if (n_logits)
         ENG_TRY(hipMemcpyAsync(logits, e.host_logits.p, n_logits * sizeof(float), hipMemcpyDeviceToHost, e.stream),
                 "logits download");
@@ -571,7 +618,14 @@ extern "C" int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T, 
 
 extern "C" int yuf_step_device(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens_dev,
                                float *logits_dev) {
-    return yuf_prefill_device(eng, n, slots, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
+    using namespace yuf;
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    Engine &e = eng->e;
+    int rc = check_slots(e, n, slots);
+    if (rc != YUF_OK) return rc;
+    if (!tokens_dev || !logits_dev) return fail(YUF_ERR_INVALID, "null buffer");
+    if ((rc = upload_slots(e, n, slots)) != YUF_OK) return rc;
+    return step_impl(e, n, tokens_dev, logits_dev);
 }
 
 extern "C" int yuf_step(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens, float *logits) {

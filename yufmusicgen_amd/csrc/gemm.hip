@@ -421,6 +421,98 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
 }
 
 // ---------------------------------------------------------------------------
+// Decode path (M <= 64 rows, one token per stream): the product streams W once
+// and is latency-bound, so a workgroup of 8 waves owns a 16-column slice of
+// the output (two slices, in + gate, for the paired SiLU layout) and splits K
+// eight ways inside the workgroup; the eight partial 64 x 16 tiles are summed
+// in LDS in a fixed order and the epilogue is applied once.  No workspace, no
+// second kernel.  Each wave: 4 m-tiles of v_mfma_f32_16x16x4f32 per 16-column
+// slice, A and W read straight from global memory as 16-byte runs (rows past
+// M and k past K read as zero through the buffer descriptors).
+// ---------------------------------------------------------------------------
+constexpr int kDecWaves = 8, kDecThreads = kDecWaves * 64, kDecRows = 64;
+
+template <int NT>
+__global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(GemmGroup g) {
+    __shared__ __attribute__((aligned(16))) float red[kDecWaves][NT][kDecRows * 17];
+    const GemmParams &p = g.p[blockIdx.y];
+    const int slice = blockIdx.x;
+    // Output columns of this workgroup: NT = 1 -> 16 consecutive W rows; NT = 2
+    // (SiLU pair) -> rows c and c + 32 of one 64-row [in | gate] block.
+    const int w_row0 = NT == 1 ? slice * 16 : (slice / 2) * 64 + (slice % 2) * 16;
+    if (w_row0 >= p.N) return;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g4 = lane >> 4, li = lane & 15;
+    const int kc = ((p.K + kDecWaves * 16 - 1) / (kDecWaves * 16)) * 16;  // k per wave, multiple of 16
+    const int k_begin = wave * kc, k_end = min(p.K, k_begin + kc);
+    const int rows = min(p.M, kDecRows);
+    const auto ra = make_rsrc(p.A, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
+    const auto rw = make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 4));
+
+    floatx4 acc[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = k_begin; k0 < k_end; k0 += 16) {
+        const int k = k0 + 4 * g4;
+        const bool kin = k < k_end;  // K % 4 == 0 on this path
+        floatx4 a[4], b[NT];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 16 * i + li;
+            a[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   ra, kin ? (uint32_t)((size_t)row * p.lda + k) * 4u : kBufferOob, 0, 0));
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int wr = w_row0 + 32 * t + li;
+            b[t] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob, 0, 0));
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][r], b[t][r], acc[t][i], 0, 0, 0);
+    }
+    // Register r of lane l in m-tile i: row 16 i + 4 (l / 16) + r, column l % 16.
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) red[wave][t][(16 * i + 4 * g4 + r) * 17 + li] = acc[t][i][r];
+    lds_barrier();
+    // 64 rows x 16 columns per slice: thread -> (row, column) pairs, waves summed in order.
+    for (int q = tid; q < kDecRows * 16; q += kDecThreads) {
+        const int row = q >> 4, c = q & 15;
+        if (row >= p.M) continue;
+        float x[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) sum += red[w][t][row * 17 + c];
+            x[t] = sum;
+        }
+        if constexpr (NT == 2) {
+            const int hcol = (w_row0 / 64) * 32 + (w_row0 % 64) + c;
+            p.C[(size_t)row * p.ldc + hcol] = x[0] / (1.0f + expf(-x[0])) * x[NT - 1];
+        } else {
+            const int col = w_row0 + c;
+            if (col < p.N) {
+                float y = apply_act(x[0] + (p.bias ? p.bias[col] : 0.0f), p.act);
+                if (p.residual) y += p.residual[(size_t)row * p.ldr + col];
+                p.C[(size_t)row * p.ldc + col] = y;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Short-M path (decode: M <= 64 rows, one token per stream).  The product is
 // bound by streaming W from HBM, so parallelism comes from N and K instead of
 // M: each wave owns 64 rows x 64 columns (2 x 2 MFMA 32x32 tiles) over a K
@@ -584,6 +676,24 @@ void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStre
         hipLaunchKernelGGL((gemm_big_kernel<BN, false>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
 }
 
+// Decode products (M <= 64, K % 4 == 0): one launch per group; all products of
+// a group share the SiLU-pair flag.
+hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
+    GemmGroup g{};
+    int max_slices = 0;
+    for (int i = 0; i < count; ++i) {
+        g.p[i] = ps[i];
+        const int slices = ps[i].silu_pair ? ps[i].N / 32 : (ps[i].N + 15) / 16;
+        max_slices = std::max(max_slices, slices);
+    }
+    const dim3 grid(max_slices, count), block(kDecThreads);
+    if (ps[0].silu_pair) hipLaunchKernelGGL(gemm_decode_kernel<2>, grid, block, 0, stream, g);
+    else hipLaunchKernelGGL(gemm_decode_kernel<1>, grid, block, 0, stream, g);
+    return hipGetLastError();
+}
+
+bool decode_ok(const GemmParams &p) { return p.M <= 64 && p.K % 4 == 0; }
+
 int skinny_splits(int N, int K) {
     const int wave_tiles = (N + 63) / 64;
     const int max_splits = (K + 31) / 32;
@@ -600,6 +710,7 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
     // Buffer descriptors address at most 2^31 bytes per 128-row panel.
     if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
+    if (decode_ok(p)) return launch_decode(&p, 1, stream);
     if (p.M <= 64) {
         int splits = skinny_splits(p.N, p.K);
         if (!p.workspace || (size_t)splits * p.M * p.N > p.workspace_floats) splits = 1;
@@ -620,11 +731,29 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
 
 hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream) {
     if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
+    {
+        // Decode-shaped products: grouped by the SiLU flag into one launch each.
+        GemmParams dec[2][kMaxGroup];
+        int nd[2] = {0, 0};
+        for (int i = 0; i < count; ++i) {
+            const GemmParams &p = ps[i];
+            if (p.M <= 0 || p.N <= 0 || !decode_ok(p)) continue;
+            if (p.K <= 0 || p.lda < p.K || p.ldw < p.K) return hipErrorInvalidValue;
+            if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
+            dec[p.silu_pair ? 1 : 0][nd[p.silu_pair ? 1 : 0]++] = p;
+        }
+        for (int f = 0; f < 2; ++f)
+            if (nd[f] > 0) {
+                hipError_t e = launch_decode(dec[f], nd[f], stream);
+                if (e != hipSuccess) return e;
+            }
+    }
     GemmGroup g{};
     int max_total = 0, n = 0;
     for (int i = 0; i < count; ++i) {
         const GemmParams &p = ps[i];
         if (p.M <= 0 || p.N <= 0) continue;
+        if (decode_ok(p)) continue;  // launched above
         if (p.M <= 64) {  // short-M products take the split-K path one by one
             hipError_t e = launch_gemm(p, stream);
             if (e != hipSuccess) return e;
