@@ -248,10 +248,6 @@ int gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W
 // Several independent products in one launch (the short-M split-K path runs
 // them one after another: its workspace holds one product at a time).
 int gemm_group(Engine &e, const GemmParams *ps, int count) {
-    if (ps[0].M <= 64) {
-        for (int i = 0; i < count; ++i) ENG_TRY(launch_gemm(ps[i], e.stream), "gemm");
-        return YUF_OK;
-    }
     ENG_TRY(launch_gemm_group(ps, count, e.stream), "gemm group");
     return YUF_OK;
 }

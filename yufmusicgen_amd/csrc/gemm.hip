@@ -422,15 +422,16 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
 
 // ---------------------------------------------------------------------------
 // Decode path (M <= 64 rows, one token per stream): the product streams W once
-// and is latency-bound, so a workgroup of 8 waves owns a 16-column slice of
+// and is latency-bound, so a workgroup of 16 waves owns a 16-column slice of
 // the output (two slices, in + gate, for the paired SiLU layout) and splits K
-// eight ways inside the workgroup; the eight partial 64 x 16 tiles are summed
+// sixteen ways inside the workgroup (each wave's loads run one 16-k step ahead
+// of its MFMAs); the partial 64 x 16 tiles are summed
 // in LDS in a fixed order and the epilogue is applied once.  No workspace, no
 // second kernel.  Each wave: 4 m-tiles of v_mfma_f32_16x16x4f32 per 16-column
 // slice, A and W read straight from global memory as 16-byte runs (rows past
 // M and k past K read as zero through the buffer descriptors).
 // ---------------------------------------------------------------------------
-constexpr int kDecWaves = 8, kDecThreads = kDecWaves * 64, kDecRows = 64;
+constexpr int kDecWaves = 16, kDecThreads = kDecWaves * 64, kDecRows = 64;
 
 template <int NT>
 __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(GemmGroup g) {
@@ -454,22 +455,27 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(GemmGroup g) {
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = k_begin; k0 < k_end; k0 += 16) {
+    floatx4 a[4], b[NT], an[4], bn[NT];
+    auto load_step = [&](int k0, floatx4 (&ad)[4], floatx4 (&bd)[NT]) {
         const int k = k0 + 4 * g4;
         const bool kin = k < k_end;  // K % 4 == 0 on this path
-        floatx4 a[4], b[NT];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 16 * i + li;
-            a[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   ra, kin ? (uint32_t)((size_t)row * p.lda + k) * 4u : kBufferOob, 0, 0));
+            ad[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    ra, kin ? (uint32_t)((size_t)row * p.lda + k) * 4u : kBufferOob, 0, 0));
         }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int wr = w_row0 + 32 * t + li;
-            b[t] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob, 0, 0));
+            bd[t] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                    rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob, 0, 0));
         }
+    };
+    if (k_begin < k_end) load_step(k_begin, a, b);
+    for (int k0 = k_begin; k0 < k_end; k0 += 16) {
+        const bool more = k0 + 16 < k_end;
+        if (more) load_step(k0 + 16, an, bn);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -477,6 +483,12 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(GemmGroup g) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][r], b[t][r], acc[t][i], 0, 0, 0);
+        if (more) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = an[i];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) b[t] = bn[t];
+        }
     }
     // Register r of lane l in m-tile i: row 16 i + 4 (l / 16) + r, column l % 16.
 #pragma unroll
