@@ -176,12 +176,14 @@ def test_device_sampling():
     assert float((emp - p).abs().sum()) < 0.5
 
 
-def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch):
+@pytest.mark.parametrize("preset", ["tiny", "0.1b"])
+def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, preset):
     """Decode steps replayed from the captured HIP graph equal eager steps
     bit for bit, across replays separated by other device work and host
     synchronisations, a change of batch size (re-capture) and the host-buffer
-    entry point."""
-    cfg = PRESETS["tiny"]
+    entry point.  The 0.1B shapes exercise the grouped decode products and the
+    SiLU-paired FFN slices at their real widths."""
+    cfg = PRESETS[preset]
     path = tmp_path / "tiny.yuf"
     write_yuf(path, cfg, synth_weights(cfg, seed=3))
     ck = Checkpoint.load(path)
