@@ -154,6 +154,31 @@ def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path, steps):
     np.testing.assert_allclose(blob, state_to_blob(state), rtol=1e-4, atol=1e-4)
 
 
+def test_wide_decode_batch_vs_oracle(tmp_path):
+    """40 streams of the 0.1B architecture: the decode products take 16-row
+    tiles with a ragged last tile (16 + 16 + 8), the LayerNorm prologues, the
+    single-token WKV / ROSA kernels and, replayed from the graph, two groups
+    of 20 streams on forked HIP streams; against the float64 oracle."""
+    cfg = PRESETS["0.1b"]
+    weights = synth_weights(cfg, seed=4)
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, weights)
+    n = 40
+    tokens = uniform_tokens(7, n, 6, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=n, max_tokens=n * 6)
+    got = eng.prefill(tokens, logits="last")
+    oracle = OracleModel(cfg.to_dict(), weights)
+    ref, state = oracle.forward(tokens)
+    np.testing.assert_allclose(got, ref.numpy()[:, -1], rtol=0, atol=LOGIT_ATOL)
+    nxt = uniform_tokens(8, n, 3, cfg.vocab_size)
+    for t in range(3):
+        g = eng.step(nxt[:, t])
+        r, state = oracle.step(nxt[:, t], state)
+        np.testing.assert_allclose(g, r.numpy(), rtol=0, atol=LOGIT_ATOL, err_msg=f"step {t}")
+    blob = _states_from_blob(eng, [0, 17, 39])
+    np.testing.assert_allclose(blob, state_to_blob(state)[[0, 17, 39]], rtol=1e-4, atol=1e-4)
+
+
 def test_device_sampling():
     torch.manual_seed(0)
     logits = torch.randn(8, 20480, device="cuda") * 3
@@ -176,17 +201,20 @@ def test_device_sampling():
     assert float((emp - p).abs().sum()) < 0.5
 
 
-@pytest.mark.parametrize("preset", ["tiny", "0.1b"])
-def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, preset):
+@pytest.mark.parametrize("preset,branches", [("tiny", 1), ("tiny", 2), ("tiny", 3), ("0.1b", 2), ("0.1b", 4)])
+def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, preset, branches):
     """Decode steps replayed from the captured HIP graph equal eager steps
     bit for bit, across replays separated by other device work and host
     synchronisations, a change of batch size (re-capture) and the host-buffer
-    entry point.  The 0.1B shapes exercise the grouped decode products and the
-    SiLU-paired FFN slices at their real widths."""
+    entry point.  The graph splits the streams into `branches` groups recorded
+    on forked HIP streams (uneven groups included); the eager engine runs the
+    whole batch as one pass.  The 0.1B shapes exercise the grouped decode
+    products and the SiLU-paired FFN slices at their real widths."""
     cfg = PRESETS[preset]
     path = tmp_path / "tiny.yuf"
     write_yuf(path, cfg, synth_weights(cfg, seed=3))
     ck = Checkpoint.load(path)
+    monkeypatch.setenv("YUF_DECODE_BRANCHES", str(branches))
     graph_eng = Engine(ck, max_streams=4, max_tokens=128)
     monkeypatch.setenv("YUF_NO_GRAPH", "1")
     eager_eng = Engine(ck, max_streams=4, max_tokens=128)

@@ -53,6 +53,63 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const float *x, int M, i
     }
 }
 
+// Single-token step (T = 1): LayerNorm of row b, the six token-shift mixes
+// against prev_state[slot[b]] (as token_shift_kernel), and prev_state[slot[b]]
+// <- the normed row (yufmusicgen/model.py:97-105, :197), one 256-thread
+// workgroup per row.  Every load (row, previous row, affine, mixes) is issued
+// before the first store, so the kernel costs one memory round trip; each
+// thread reads a column's previous value before it overwrites it.
+template <int PER>
+__global__ void __launch_bounds__(256) ln_shift_kernel(const float *__restrict__ x, int d,
+                                                       const float *__restrict__ gamma,
+                                                       const float *__restrict__ beta, float *__restrict__ prev_state,
+                                                       const int *__restrict__ slot, const float *__restrict__ mix6,
+                                                       float *__restrict__ out6, size_t out_stride) {
+    __shared__ float part[2][4];
+    const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const float *xr = x + (size_t)row * d;
+    float *prow = prev_state + (size_t)(slot ? slot[row] : row) * d;
+    float v[PER], pv[PER], gm[PER], bt[PER], mx[6][PER];
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = tid + e * 256;
+        const bool ok = c < d;
+        v[e] = ok ? xr[c] : 0.0f;
+        pv[e] = ok ? prow[c] : 0.0f;
+        gm[e] = ok ? gamma[c] : 0.0f;
+        bt[e] = ok ? beta[c] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 6; ++q) mx[q][e] = ok ? mix6[q * d + c] : 0.0f;
+        sum += v[e];
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) part[0][wave] = sum;
+    lds_barrier();
+    const float mean = ((part[0][0] + part[0][1]) + (part[0][2] + part[0][3])) / (float)d;
+    float sq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const float dv = tid + e * 256 < d ? v[e] - mean : 0.0f;
+        sq = fmaf(dv, dv, sq);
+    }
+    sq = wave_sum(sq);
+    if (lane == 0) part[1][wave] = sq;
+    lds_barrier();
+    const float rstd = rsqrtf(((part[1][0] + part[1][1]) + (part[1][2] + part[1][3])) / (float)d + 1e-5f);
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = tid + e * 256;
+        if (c < d) {
+            const float xv = (v[e] - mean) * rstd * gm[e] + bt[e];
+            const float delta = xv - pv[e];
+#pragma unroll
+            for (int q = 0; q < 6; ++q) out6[q * out_stride + (size_t)row * d + c] = fmaf(delta, mx[q][e], xv);
+            prow[c] = xv;
+        }
+    }
+}
+
 __global__ void embed_kernel(const int *tokens, int M, const float *table, int d, int vocab, float *out,
                              int *bad) {
     const int row = blockIdx.x;
@@ -135,6 +192,19 @@ hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, co
     else if (per <= 16) hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
     else if (per <= kMaxPerLane)
         hipLaunchKernelGGL(layernorm_kernel<kMaxPerLane>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_shift(const float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
+                           const int *slot, const float *mix6, float *out6, size_t out_stride, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const dim3 grid(n), block(256);
+    const int per = (d + 255) / 256;
+    if (per <= 1) hipLaunchKernelGGL(ln_shift_kernel<1>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
+    else if (per <= 2) hipLaunchKernelGGL(ln_shift_kernel<2>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
+    else if (per <= 3) hipLaunchKernelGGL(ln_shift_kernel<3>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
+    else if (per <= 4) hipLaunchKernelGGL(ln_shift_kernel<4>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

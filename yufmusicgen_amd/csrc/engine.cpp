@@ -73,17 +73,30 @@ struct Engine {
     // Device staging for the host-buffer entry points (grown on demand).
     DeviceBuf host_tokens, host_logits;
     size_t host_tokens_cap = 0, host_logits_cap = 0;
-    // Decode step captured as a HIP graph (~30 kernels per layer replayed with
-    // one launch); rebuilt when n or the token / logit buffers change.
+    // Decode step captured as a HIP graph (about ten kernels per layer and
+    // group, replayed with one launch); rebuilt when n or the token / logit
+    // buffers change.
     // YUF_NO_GRAPH=1 runs every step eagerly.
     bool use_graphs = true;
     hipGraphExec_t step_exec = nullptr;
     int step_n = 0;
     const int32_t *step_tok = nullptr;
     float *step_logits = nullptr;
+    // The captured step splits its streams into `branches` groups recorded on
+    // their own HIP streams (fork / join events): independent chains of small
+    // kernels that the GPU overlaps.  YUF_DECODE_BRANCHES=1..4 overrides.
+    static constexpr int kMaxBranches = 4;
+    int branches = 1;
+    hipStream_t side[kMaxBranches - 1] = {};
+    hipEvent_t fork = nullptr, join[kMaxBranches - 1] = {};
 
     ~Engine() {
         if (step_exec) (void)hipGraphExecDestroy(step_exec);
+        for (int i = 0; i < kMaxBranches - 1; ++i) {
+            if (side[i]) (void)hipStreamDestroy(side[i]);
+            if (join[i]) (void)hipEventDestroy(join[i]);
+        }
+        if (fork) (void)hipEventDestroy(fork);
         if (stream) {
             (void)hipStreamSynchronize(stream);
             (void)hipStreamDestroy(stream);
@@ -237,94 +250,165 @@ GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, co
     return p;
 }
 
-int gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C, int ldc,
-         const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr, int ldr = 0,
+int gemm(Engine &e, hipStream_t st, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C,
+         int ldc, const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr, int ldr = 0,
          bool silu_pair = false) {
-    ENG_TRY(launch_gemm(make_gemm(e, M, N, K, A, lda, W, ldw, C, ldc, bias, act, residual, ldr, silu_pair), e.stream),
+    ENG_TRY(launch_gemm(make_gemm(e, M, N, K, A, lda, W, ldw, C, ldc, bias, act, residual, ldr, silu_pair), st),
             "gemm");
     return YUF_OK;
 }
 
+// LayerNorm(A) [* gate] -> Linear.  Short products (M <= 64) fold the norm into
+// the GEMM's A prologue; otherwise -- and for the wide LM head, whose many
+// workgroups would each recompute the row statistics -- the normed rows go
+// through `scratch` first.
+int ln_gemm(Engine &e, hipStream_t st, int M, int N, int K, const float *A, int lda, const float *gamma,
+            const float *beta, const float *gate, float *scratch, const float *W, float *C, int ldc,
+            const float *bias = nullptr, const float *residual = nullptr, int ldr = 0, bool silu_pair = false) {
+    if (M <= 64 && K % 4 == 0 && K <= 1024 && N <= 8192) {
+        GemmParams p = make_gemm(e, M, N, K, A, lda, W, K, C, ldc, bias, ACT_NONE, residual, ldr, silu_pair);
+        p.ln_gamma = gamma; p.ln_beta = beta; p.a_gate = gate; p.ldg = gate ? lda : 0;
+        ENG_TRY(launch_gemm(p, st), "ln gemm");
+        return YUF_OK;
+    }
+    if (lda != K) return fail(YUF_ERR_INVALID, "ln_gemm: strided rows need the fused path");
+    ENG_TRY(launch_layernorm(A, M, K, gamma, beta, gate, scratch, st), "layernorm");
+    return gemm(e, st, M, N, K, scratch, K, W, K, C, ldc, bias, ACT_NONE, residual, ldr, silu_pair);
+}
+
 // Several independent products in one launch (the short-M split-K path runs
 // them one after another: its workspace holds one product at a time).
-int gemm_group(Engine &e, const GemmParams *ps, int count) {
-    ENG_TRY(launch_gemm_group(ps, count, e.stream), "gemm group");
+int gemm_group(hipStream_t st, const GemmParams *ps, int count) {
+    ENG_TRY(launch_gemm_group(ps, count, st), "gemm group");
     return YUF_OK;
 }
 
-// One forward pass over n streams x Tc tokens already in e.tokens_dev / e.slots_dev.
-// logits: LAST -> [n, V] at `logits`; ALL -> row (b, t) at logits + (b * row_stride_T + t0 + t) * V.
-int forward_pass(Engine &e, int n, int Tc, float *logits, int mode, int row_stride_T, int t0) {
+// The activation rows of one forward pass: the engine's workspace from stream
+// s0 on (token row s0 * Tc), and the HIP stream its kernels go to.  A decode
+// step splits its batch into groups of streams whose passes touch disjoint
+// rows, so they can run as parallel branches of one graph.
+struct Act {
+    hipStream_t st = nullptr;
+    float *h, *xn, *mix, *r, *k, *v, *wr, *al, *g, *lr, *y, *z, *rosa3, *rread, *ffn, *hl;
+    const int *tokens, *slots;
+};
+
+Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
+    const ModelShape &s = e.s;
+    const size_t m0 = (size_t)s0 * Tc, d = s.d;
+    Act a;
+    a.st = st;
+    a.h = e.h + m0 * d; a.xn = e.xn + m0 * d; a.mix = e.mix + m0 * d;
+    a.r = e.r + m0 * d; a.k = e.k + m0 * d; a.v = e.v + m0 * d; a.wr = e.wr + m0 * d; a.al = e.al + m0 * d;
+    a.g = e.g + m0 * d; a.y = e.y + m0 * d; a.z = e.z + m0 * d;
+    a.lr = e.lr + m0 * s.low_rank;
+    a.rosa3 = e.rosa3 + m0 * 3 * s.rosa; a.rread = e.rread + m0 * s.rosa;
+    a.ffn = e.ffn + m0 * 4 * d;
+    a.hl = e.hl + (size_t)s0 * d;
+    a.tokens = e.tokens_dev + m0;
+    a.slots = e.slots_dev + s0;
+    return a;
+}
+
+// Final norm and tied LM head on the last token of each of n streams.
+int lm_head_last(Engine &e, const Act &a, int n, int Tc, float *logits) {
+    const int d = e.s.d, V = e.s.vocab;
+    const float *last = a.h;
+    if (Tc > 1) {
+        ENG_TRY(launch_gather_last(a.h, n, Tc, d, a.hl, a.st), "gather_last");
+        last = a.hl;
+    }
+    return ln_gemm(e, a.st, n, V, d, last, d, e.ln_fin_w, e.ln_fin_b, nullptr, a.xn, e.head, logits, V);
+}
+
+// One forward pass over n streams x Tc tokens whose ids and slots are in
+// a.tokens / a.slots.  logits: LAST -> [n, V] at `logits`; ALL -> row (b, t) at
+// logits + (b * row_stride_T + t0 + t) * V.
+int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode, int row_stride_T, int t0) {
     const ModelShape &s = e.s;
     const int M = n * Tc, d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4 * s.d;
-    const size_t plane = (size_t)e.max_tokens * d;
-    hipStream_t st = e.stream;
-    ENG_TRY(launch_embed(e.tokens_dev, M, e.emb, d, V, e.h, e.bad_dev, st), "embed");
+    const size_t plane = (size_t)e.max_tokens * d, lplane = (size_t)e.max_tokens * L;
+    hipStream_t st = a.st;
+    ENG_TRY(launch_embed(a.tokens, M, e.emb, d, V, a.h, e.bad_dev, st), "embed");
     for (int l = 0; l < s.layers; ++l) {
         const LayerW &w = e.layers[l];
         float *prev = e.st_prev + (size_t)l * e.max_streams * d;
         float *wkv = e.st_wkv + (size_t)l * e.max_streams * e.wkv_floats();
         float *ros = e.st_rosa + (size_t)l * e.max_streams * D;
         // TimeMix
-        ENG_TRY(launch_layernorm(e.h, M, d, w.ln_t_w, w.ln_t_b, nullptr, e.xn, st), "ln_time");
-        ENG_TRY(launch_token_shift(e.xn, n, Tc, d, prev, e.slots_dev, w.mix6, e.mix, plane, st), "token_shift");
-        ENG_TRY(launch_save_prev(e.xn, n, Tc, d, prev, e.slots_dev, st), "save_prev");
-        const float *mr = e.mix, *mw = e.mix + plane, *mk = e.mix + 2 * plane, *mv = e.mix + 3 * plane,
-                    *ma = e.mix + 4 * plane, *mg = e.mix + 5 * plane;
+        if (Tc == 1 && d <= 1024) {
+            ENG_TRY(launch_ln_shift(a.h, n, d, w.ln_t_w, w.ln_t_b, prev, a.slots, w.mix6, a.mix, plane, st),
+                    "ln_shift");
+        } else {
+            ENG_TRY(launch_layernorm(a.h, M, d, w.ln_t_w, w.ln_t_b, nullptr, a.xn, st), "ln_time");
+            ENG_TRY(launch_token_shift(a.xn, n, Tc, d, prev, a.slots, w.mix6, a.mix, plane, st), "token_shift");
+            ENG_TRY(launch_save_prev(a.xn, n, Tc, d, prev, a.slots, st), "save_prev");
+        }
+        const float *mr = a.mix, *mw = a.mix + plane, *mk = a.mix + 2 * plane, *mv = a.mix + 3 * plane,
+                    *ma = a.mix + 4 * plane, *mg = a.mix + 5 * plane;
         int rc;
         {
-            // r, k, v in one launch; then the three low-rank first stages; then the second stages.
-            const float *lw = e.lr, *la = e.lr + (size_t)e.max_tokens * L, *lg = e.lr + 2 * (size_t)e.max_tokens * L;
-            GemmParams g3[3] = {make_gemm(e, M, d, d, mr, d, w.w_r, d, e.r, d),
-                                make_gemm(e, M, d, d, mk, d, w.w_k, d, e.k, d),
-                                make_gemm(e, M, d, d, mv, d, w.w_v, d, e.v, d)};
-            if ((rc = gemm_group(e, g3, 3)) != YUF_OK) return rc;
-            GemmParams l1[3] = {make_gemm(e, M, L, d, mw, d, w.w1t, d, const_cast<float *>(lw), L, nullptr, ACT_TANH),
-                                make_gemm(e, M, L, d, ma, d, w.a1t, d, const_cast<float *>(la), L),
-                                make_gemm(e, M, L, d, mg, d, w.g1t, d, const_cast<float *>(lg), L)};
-            if ((rc = gemm_group(e, l1, 3)) != YUF_OK) return rc;
-            GemmParams l2[3] = {make_gemm(e, M, d, L, lw, L, w.w2t, L, e.wr, d, w.w0),
-                                make_gemm(e, M, d, L, la, L, w.a2t, L, e.al, d, w.a0, ACT_SIGMOID),
-                                make_gemm(e, M, d, L, lg, L, w.g2t, L, e.g, d, nullptr, ACT_SIGMOID)};
-            if ((rc = gemm_group(e, l2, 3)) != YUF_OK) return rc;
+            // r, k, v and the three low-rank first stages (one launch for short
+            // products, two otherwise: the tile widths differ); then the second stages.
+            float *lw = a.lr, *la = a.lr + lplane, *lg = a.lr + 2 * lplane;
+            GemmParams g6[6] = {make_gemm(e, M, d, d, mr, d, w.w_r, d, a.r, d),
+                                make_gemm(e, M, d, d, mk, d, w.w_k, d, a.k, d),
+                                make_gemm(e, M, d, d, mv, d, w.w_v, d, a.v, d),
+                                make_gemm(e, M, L, d, mw, d, w.w1t, d, lw, L, nullptr, ACT_TANH),
+                                make_gemm(e, M, L, d, ma, d, w.a1t, d, la, L),
+                                make_gemm(e, M, L, d, mg, d, w.g1t, d, lg, L)};
+            if (M <= 64) {
+                if ((rc = gemm_group(st, g6, 6)) != YUF_OK) return rc;
+            } else {
+                if ((rc = gemm_group(st, g6, 3)) != YUF_OK) return rc;
+                if ((rc = gemm_group(st, g6 + 3, 3)) != YUF_OK) return rc;
+            }
+            GemmParams l2[3] = {make_gemm(e, M, d, L, lw, L, w.w2t, L, a.wr, d, w.w0),
+                                make_gemm(e, M, d, L, la, L, w.a2t, L, a.al, d, w.a0, ACT_SIGMOID),
+                                make_gemm(e, M, d, L, lg, L, w.g2t, L, a.g, d, nullptr, ACT_SIGMOID)};
+            if ((rc = gemm_group(st, l2, 3)) != YUF_OK) return rc;
         }
         WkvParams wp;
         wp.B = n; wp.T = Tc; wp.H = s.heads;
-        wp.r = e.r; wp.w = e.wr; wp.k = e.k; wp.v = e.v; wp.a = e.al;
+        wp.r = a.r; wp.w = a.wr; wp.k = a.k; wp.v = a.v; wp.a = a.al;
         wp.k_k = w.k_k; wp.k_a = w.k_a;
-        wp.state_in = wkv; wp.state_out = wkv; wp.slot = e.slots_dev; wp.y = e.y;
+        wp.state_in = wkv; wp.state_out = wkv; wp.slot = a.slots; wp.y = a.y;
         ENG_TRY(launch_wkv7(wp, s.head_size, true, st), "wkv7");
-        ENG_TRY(launch_layernorm(e.y, M, d, w.ln_o_w, w.ln_o_b, e.g, e.z, st), "ln_out");
-        if ((rc = gemm(e, M, d, d, e.z, d, w.w_o, d, e.h, d, nullptr, ACT_NONE, e.h, d)) != YUF_OK) return rc;
+        if ((rc = ln_gemm(e, st, M, d, d, a.y, d, w.ln_o_w, w.ln_o_b, a.g, a.z, w.w_o, a.h, d, nullptr, a.h, d)) !=
+            YUF_OK)
+            return rc;
         // ROSA
-        ENG_TRY(launch_layernorm(e.h, M, d, w.ln_r_w, w.ln_r_b, nullptr, e.xn, st), "ln_rosa");
-        if ((rc = gemm(e, M, 3 * D, d, e.xn, d, w.rosa_w3, d, e.rosa3, 3 * D, w.rosa_b3)) != YUF_OK) return rc;
-        // Gates on all M rows in parallel, so the sequential scan only loads e and the gate.
-        ENG_TRY(launch_rosa_gates(e.rosa3, M, D, 3 * D, st), "rosa_gates");
+        if ((rc = ln_gemm(e, st, M, 3 * D, d, a.h, d, w.ln_r_w, w.ln_r_b, nullptr, a.xn, w.rosa_w3, a.rosa3, 3 * D,
+                          w.rosa_b3)) != YUF_OK)
+            return rc;
         RosaParams rp;
         rp.B = n; rp.T = Tc; rp.D = D; rp.ld = 3 * D;
-        rp.e_pre = e.rosa3; rp.g_pre = e.rosa3 + D;
+        if (Tc == 1) {
+            // The single-token kernel applies the gates itself.
+            rp.cand = a.rosa3; rp.write = a.rosa3 + D; rp.read_raw = a.rosa3 + 2 * D;
+        } else {
+            // Gates on all M rows in parallel, so the sequential scan only loads e and the gate.
+            ENG_TRY(launch_rosa_gates(a.rosa3, M, D, 3 * D, st), "rosa_gates");
+            rp.e_pre = a.rosa3; rp.g_pre = a.rosa3 + D;
+        }
         rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
-        rp.memory_in = ros; rp.memory_out = ros; rp.slot = e.slots_dev; rp.read_out = e.rread;
+        rp.memory_in = ros; rp.memory_out = ros; rp.slot = a.slots; rp.read_out = a.rread;
         ENG_TRY(launch_rosa(rp, st), "rosa");
-        if ((rc = gemm(e, M, d, D, e.rread, D, w.rosa_out, D, e.h, d, nullptr, ACT_NONE, e.h, d)) != YUF_OK) return rc;
+        if ((rc = gemm(e, st, M, d, D, a.rread, D, w.rosa_out, D, a.h, d, nullptr, ACT_NONE, a.h, d)) != YUF_OK)
+            return rc;
         // FFN
-        ENG_TRY(launch_layernorm(e.h, M, d, w.ln_f_w, w.ln_f_b, nullptr, e.xn, st), "ln_ffn");
-        if ((rc = gemm(e, M, 2 * hid, d, e.xn, d, w.ffn_cat, d, e.ffn, hid, nullptr, ACT_NONE, nullptr, 0, true)) != YUF_OK)
+        if ((rc = ln_gemm(e, st, M, 2 * hid, d, a.h, d, w.ln_f_w, w.ln_f_b, nullptr, a.xn, w.ffn_cat, a.ffn, hid,
+                          nullptr, nullptr, 0, true)) != YUF_OK)
             return rc;
-        if ((rc = gemm(e, M, d, hid, e.ffn, hid, w.ffn_out, hid, e.h, d, nullptr, ACT_NONE, e.h, d)) != YUF_OK)
+        if ((rc = gemm(e, st, M, d, hid, a.ffn, hid, w.ffn_out, hid, a.h, d, nullptr, ACT_NONE, a.h, d)) != YUF_OK)
             return rc;
     }
-    if (mode == YUF_LOGITS_LAST) {
-        ENG_TRY(launch_gather_last(e.h, n, Tc, d, e.hl, st), "gather_last");
-        ENG_TRY(launch_layernorm(e.hl, n, d, e.ln_fin_w, e.ln_fin_b, nullptr, e.xn, st), "ln_final");
-        return gemm(e, n, V, d, e.xn, d, e.head, d, logits, V);
-    }
+    if (mode == YUF_LOGITS_LAST) return lm_head_last(e, a, n, Tc, logits);
     if (mode == YUF_LOGITS_ALL) {
-        ENG_TRY(launch_layernorm(e.h, M, d, e.ln_fin_w, e.ln_fin_b, nullptr, e.xn, st), "ln_final");
-        if (row_stride_T == Tc && t0 == 0) return gemm(e, M, V, d, e.xn, d, e.head, d, logits, V);
+        ENG_TRY(launch_layernorm(a.h, M, d, e.ln_fin_w, e.ln_fin_b, nullptr, a.xn, st), "ln_final");
+        if (row_stride_T == Tc && t0 == 0) return gemm(e, st, M, V, d, a.xn, d, e.head, d, logits, V);
         for (int b = 0; b < n; ++b) {
-            int rc = gemm(e, Tc, V, d, e.xn + (size_t)b * Tc * d, d, e.head, d,
+            int rc = gemm(e, st, Tc, V, d, a.xn + (size_t)b * Tc * d, d, e.head, d,
                           logits + ((size_t)b * row_stride_T + t0) * V, V);
             if (rc != YUF_OK) return rc;
         }
@@ -372,7 +456,7 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         }
         const bool last_chunk = t0 + tc >= T;
         const int chunk_mode = mode == YUF_LOGITS_ALL ? YUF_LOGITS_ALL : (last_chunk ? mode : YUF_LOGITS_NONE);
-        int rc = forward_pass(e, n, tc, logits_dev, chunk_mode, T, t0);
+        int rc = forward_pass(e, act_at(e, e.stream, 0, tc), n, tc, logits_dev, chunk_mode, T, t0);
         if (rc != YUF_OK) return rc;
     }
     return YUF_OK;
@@ -382,6 +466,30 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
 // already on the device, replayed from a captured graph when possible.  The
 // captured work is kernels and one device-to-device copy only (no memset
 // nodes, no host synchronisation).
+// The work of one captured step: the token copy on the engine stream, then the
+// layers of each group of streams, group 0 on the engine stream and the others
+// on side streams forked from and joined back into it, then the final norm and
+// LM head once for all n streams (the head's weights are read once per step).
+int step_record(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
+    ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice, e.stream),
+            "tokens copy");
+    const int G = std::max(1, std::min(e.branches, n));
+    if (G == 1) return forward_pass(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev, YUF_LOGITS_LAST, 1, 0);
+    ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
+    for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.side[g - 1], e.fork, 0), "fork wait");
+    for (int g = 0; g < G; ++g) {
+        const int s0 = (int)((long long)n * g / G), s1 = (int)((long long)n * (g + 1) / G);
+        hipStream_t st = g == 0 ? e.stream : e.side[g - 1];
+        const int rc = forward_pass(e, act_at(e, st, s0, 1), s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
+        if (rc != YUF_OK) return rc;
+    }
+    for (int g = 1; g < G; ++g) {
+        ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
+        ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+    }
+    return lm_head_last(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev);
+}
+
 int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
     if (!e.use_graphs) return prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
     if (!(e.step_exec && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
@@ -390,7 +498,7 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
             e.step_exec = nullptr;
         }
         ENG_TRY(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal), "capture begin");
-        const int rc = prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
+        const int rc = step_record(e, n, tokens_dev, logits_dev);
         hipGraph_t graph = nullptr;
         const hipError_t ce = hipStreamEndCapture(e.stream, &graph);
         if (rc != YUF_OK || ce != hipSuccess) {
@@ -451,6 +559,16 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
         return fail(YUF_ERR_OOM, "out of host memory preparing weights");
     }
     ENG_TRY(hipStreamCreateWithFlags(&e.stream, hipStreamNonBlocking), "stream create");
+    // Measured on MI355X (0.1B, 64 streams): 1 branch 1.49 ms per step, 2: 1.55,
+    // 3: 1.66, 4: 2.12 -- the groups' kernels contend more than they overlap.
+    e.branches = 1;
+    if (const char *b = std::getenv("YUF_DECODE_BRANCHES")) e.branches = std::atoi(b);
+    e.branches = std::max(1, std::min(e.branches, (int)Engine::kMaxBranches));
+    for (int i = 0; i + 1 < e.branches; ++i) {
+        ENG_TRY(hipStreamCreateWithFlags(&e.side[i], hipStreamNonBlocking), "side stream create");
+        ENG_TRY(hipEventCreateWithFlags(&e.join[i], hipEventDisableTiming), "event create");
+    }
+    ENG_TRY(hipEventCreateWithFlags(&e.fork, hipEventDisableTiming), "event create");
     ENG_TRY(hipMalloc(&e.weights.p, host.size() * sizeof(float)), "weights alloc");
     ENG_TRY(hipMemcpy(e.weights.p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice), "weights upload");
     const float *base = static_cast<const float *>(e.weights.p);

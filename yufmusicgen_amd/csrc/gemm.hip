@@ -421,93 +421,193 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
 }
 
 // ---------------------------------------------------------------------------
-// Decode path (M <= 64 rows, one token per stream): the product streams W once
-// and is latency-bound, so a workgroup of 16 waves owns a 16-column slice of
-// the output (two slices, in + gate, for the paired SiLU layout) and splits K
-// sixteen ways inside the workgroup (each wave's loads run one 16-k step ahead
-// of its MFMAs); the partial 64 x 16 tiles are summed
-// in LDS in a fixed order and the epilogue is applied once.  No workspace, no
-// second kernel.  Each wave: 4 m-tiles of v_mfma_f32_16x16x4f32 per 16-column
-// slice, A and W read straight from global memory as 16-byte runs (rows past
-// M and k past K read as zero through the buffer descriptors).
+// Decode path (M <= 64 rows, one token per stream).  The product is latency-
+// bound, so the unit of work is small: one workgroup owns a 16-column slice of
+// the output (two slices, in + gate, for the paired SiLU layout) for a tile of
+// 16 * MI rows, and the 8 waves of the workgroup split K.  A 64-row,
+// 640-column product is then 160 workgroups (MI = 1) instead of 40.  The row
+// tiles of one slice are dealt to the same XCD, so its W rows come from HBM
+// once and then hit that XCD's L2.  A wave issues the loads of up to S 16-k
+// steps before its first MFMA (v_mfma_f32_16x16x4f32, A and W straight from
+// global memory as 16-byte runs; rows past M and k past K read as zero through
+// the buffer descriptors), so a wave's whole K range is in flight at once.
+// The 8 partial tiles are summed in LDS in a fixed order and the epilogue is
+// applied once: no workspace, no second kernel.  Up to kMaxDecode independent
+// products with the same flags share one launch through a flat unit index.
+//
+// Optional A-side prologue (PRO): LayerNorm over the K columns of each A row
+// (eps 1e-5; the same float expressions as layernorm_kernel, so the result
+// equals LN-then-GEMM) and, for PRO = 2, an elementwise gate:
+//   A' = (LN(A) * gamma + beta) [* gate],
+// so the LN -> Linear pairs of a block run as one kernel
+// (yufmusicgen/model.py:195-196 out_norm * g -> output, :306 ROSA norm,
+// :377 FFN norm, :390-391 final norm -> LM head).
 // ---------------------------------------------------------------------------
-constexpr int kDecWaves = 16, kDecThreads = kDecWaves * 64, kDecRows = 64;
+constexpr int kDecWaves = 8, kDecThreads = kDecWaves * 64;
+constexpr int kMaxDecode = kMaxGroup;
+constexpr int kDecLnPerLane = 16;  // LayerNorm prologue: K <= 1024
 
-template <int NT>
-__global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(GemmGroup g) {
-    __shared__ __attribute__((aligned(16))) float red[kDecWaves][NT][kDecRows * 17];
-    const GemmParams &p = g.p[blockIdx.y];
-    const int slice = blockIdx.x;
-    // Output columns of this workgroup: NT = 1 -> 16 consecutive W rows; NT = 2
-    // (SiLU pair) -> rows c and c + 32 of one 64-row [in | gate] block.
+struct DecodeGroup {
+    GemmParams p[kMaxDecode];
+    int unit_end[kMaxDecode];  // running sum of units (slice x row tile) per product
+    int mtiles[kMaxDecode];    // row tiles per product
+    int count, units, per_xcd;
+};
+
+// Largest S (16-k steps in flight per wave) that keeps the prefetched operands
+// within the register budget of a 1024-thread workgroup (128 VGPRs per lane).
+constexpr int dec_cap(int NT, int MI, int PRO) {
+    return MI == 1 ? (NT == 1 && PRO < 2 ? 10 : 6) : (NT == 1 ? (PRO == 0 ? 4 : 3) : 3);
+}
+
+template <int NT, int MI, int S, int PRO>
+__global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g) {
+    constexpr int RT = 16 * MI;  // rows per workgroup
+    __shared__ __attribute__((aligned(16))) float red[kDecWaves][NT][RT * 17];
+    __shared__ float stats[PRO > 0 ? RT : 1][2];
+    __shared__ __attribute__((aligned(16))) float affine[PRO > 0 ? 2 * 64 * kDecLnPerLane : 4];  // gamma | beta
+
+    const int u = (blockIdx.x % kXcds) * g.per_xcd + blockIdx.x / kXcds;
+    if (u >= g.units) return;
+    int pi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxDecode; ++i) pi += (i < g.count && u >= g.unit_end[i - 1]) ? 1 : 0;
+    const GemmParams &p = g.p[pi];
+    const int local = u - (pi > 0 ? g.unit_end[pi - 1] : 0);
+    const int slice = local / g.mtiles[pi], mt = local - slice * g.mtiles[pi];
+    // NT = 1 -> 16 consecutive W rows; NT = 2 (SiLU pair) -> rows c and c + 32
+    // of one 64-row [in | gate] block.
     const int w_row0 = NT == 1 ? slice * 16 : (slice / 2) * 64 + (slice % 2) * 16;
-    if (w_row0 >= p.N) return;
+    const int row0 = mt * RT;
+    const int rows = min(p.M - row0, RT);
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int g4 = lane >> 4, li = lane & 15;
-    const int kc = ((p.K + kDecWaves * 16 - 1) / (kDecWaves * 16)) * 16;  // k per wave, multiple of 16
-    const int k_begin = wave * kc, k_end = min(p.K, k_begin + kc);
-    const int rows = min(p.M, kDecRows);
-    const auto ra = make_rsrc(p.A, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
+    const int spw = ((p.K + 15) / 16 + kDecWaves - 1) / kDecWaves;  // 16-k steps per wave
+    const int k_begin = min(p.K, wave * spw * 16), k_end = min(p.K, k_begin + spw * 16);
+    const auto ra = make_rsrc(p.A + (size_t)row0 * p.lda, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
     const auto rw = make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 4));
 
-    floatx4 acc[NT][4];
+    floatx4 acc[NT][MI];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    floatx4 a[4], b[NT], an[4], bn[NT];
-    auto load_step = [&](int k0, floatx4 (&ad)[4], floatx4 (&bd)[NT]) {
-        const int k = k0 + 4 * g4;
-        const bool kin = k < k_end;  // K % 4 == 0 on this path
+        for (int i = 0; i < MI; ++i) acc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    floatx4 a[S][MI], b[S][NT];
+    floatx4 gt[PRO == 2 ? S : 1][MI];
+    auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+        return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    };
+    auto load_round = [&](int k0) {
+        const auto rt = make_rsrc(PRO == 2 ? p.a_gate + (size_t)row0 * p.ldg : nullptr,
+                                  PRO == 2 ? (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4) : 0u);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int row = 16 * i + li;
-            ad[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    ra, kin ? (uint32_t)((size_t)row * p.lda + k) * 4u : kBufferOob, 0, 0));
-        }
+        for (int s = 0; s < S; ++s) {
+            const int k = k0 + 16 * s + 4 * g4;
+            const bool kin = k < k_end;  // K % 4 == 0 on this path
 #pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const int wr = w_row0 + 32 * t + li;
-            bd[t] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                    rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob, 0, 0));
+            for (int t = 0; t < NT; ++t) {
+                const int wr = w_row0 + 32 * t + li;
+                b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+                a[s][i] = load4(ra, kin ? (uint32_t)((size_t)(16 * i + li) * p.lda + k) * 4u : kBufferOob);
+            if constexpr (PRO == 2) {
+#pragma unroll
+                for (int i = 0; i < MI; ++i)
+                    gt[s][i] = load4(rt, kin ? (uint32_t)((size_t)(16 * i + li) * p.ldg + k) * 4u : kBufferOob);
+            }
         }
     };
-    if (k_begin < k_end) load_step(k_begin, a, b);
-    for (int k0 = k_begin; k0 < k_end; k0 += 16) {
-        const bool more = k0 + 16 < k_end;
-        if (more) load_step(k0 + 16, an, bn);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i][r], b[t][r], acc[t][i], 0, 0, 0);
-        if (more) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = an[i];
-#pragma unroll
-            for (int t = 0; t < NT; ++t) b[t] = bn[t];
+    load_round(k_begin);
+
+    float mean[MI], rstd[MI];
+    if constexpr (PRO > 0) {
+        // gamma and beta of the K columns, shared by every row of the tile.
+        for (int c = tid; c < p.K; c += kDecThreads) {
+            affine[c] = p.ln_gamma[c];
+            affine[64 * kDecLnPerLane + c] = p.ln_beta[c];
         }
+        // Row statistics: wave w normalises rows w, w + 16, ... of the tile.
+        for (int rr = wave; rr < RT; rr += kDecWaves) {
+            float v[kDecLnPerLane];
+            float sum = 0.0f;
+#pragma unroll
+            for (int e = 0; e < kDecLnPerLane; ++e) {
+                const int c = lane + e * 64;
+                v[e] = buf_load(ra, c < p.K ? (uint32_t)((size_t)rr * p.lda + c) * 4u : kBufferOob);
+                sum += v[e];
+            }
+            const float mu = wave_sum(sum) / (float)p.K;
+            float sq = 0.0f;
+#pragma unroll
+            for (int e = 0; e < kDecLnPerLane; ++e) {
+                const int c = lane + e * 64;
+                const float dv = c < p.K ? v[e] - mu : 0.0f;
+                sq = fmaf(dv, dv, sq);
+            }
+            const float rs = rsqrtf(wave_sum(sq) / (float)p.K + 1e-5f);
+            if (lane == 0) {
+                stats[rr][0] = mu;
+                stats[rr][1] = rs;
+            }
+        }
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < MI; ++i) {
+            mean[i] = stats[16 * i + li][0];
+            rstd[i] = stats[16 * i + li][1];
+        }
+    }
+
+    for (int k0 = k_begin;;) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            if constexpr (PRO > 0) {
+                const int k = k0 + 16 * s + 4 * g4;
+                if (k < k_end) {
+                    const floatx4 gm = *reinterpret_cast<const floatx4 *>(affine + k);
+                    const floatx4 bt = *reinterpret_cast<const floatx4 *>(affine + 64 * kDecLnPerLane + k);
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            float y = (a[s][i][q] - mean[i]) * rstd[i] * gm[q] + bt[q];
+                            if constexpr (PRO == 2) y *= gt[s][i][q];
+                            a[s][i][q] = y;
+                        }
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int i = 0; i < MI; ++i)
+                        acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s][i][r], b[s][t][r], acc[t][i], 0, 0, 0);
+        }
+        k0 += 16 * S;
+        if (k0 >= k_end) break;
+        load_round(k0);
     }
     // Register r of lane l in m-tile i: row 16 i + 4 (l / 16) + r, column l % 16.
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) red[wave][t][(16 * i + 4 * g4 + r) * 17 + li] = acc[t][i][r];
     lds_barrier();
-    // 64 rows x 16 columns per slice: thread -> (row, column) pairs, waves summed in order.
-    for (int q = tid; q < kDecRows * 16; q += kDecThreads) {
-        const int row = q >> 4, c = q & 15;
-        if (row >= p.M) continue;
+    for (int q = tid; q < RT * 16; q += kDecThreads) {
+        const int rl = q >> 4, c = q & 15;
+        if (rl >= rows) continue;
+        const int row = row0 + rl;
         float x[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             float sum = 0.0f;
 #pragma unroll
-            for (int w = 0; w < kDecWaves; ++w) sum += red[w][t][row * 17 + c];
+            for (int w = 0; w < kDecWaves; ++w) sum += red[w][t][rl * 17 + c];
             x[t] = sum;
         }
         if constexpr (NT == 2) {
@@ -688,23 +788,89 @@ void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStre
         hipLaunchKernelGGL((gemm_big_kernel<BN, false>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
 }
 
-// Decode products (M <= 64, K % 4 == 0): one launch per group; all products of
-// a group share the SiLU-pair flag.
-hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
-    GemmGroup g{};
-    int max_slices = 0;
-    for (int i = 0; i < count; ++i) {
-        g.p[i] = ps[i];
-        const int slices = ps[i].silu_pair ? ps[i].N / 32 : (ps[i].N + 15) / 16;
-        max_slices = std::max(max_slices, slices);
+template <int NT, int MI, int PRO, int S>
+void launch_dec_s(const DecodeGroup &g, dim3 grid, hipStream_t stream) {
+    if constexpr (S <= dec_cap(NT, MI, PRO))
+        hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO>), grid, dim3(kDecThreads), 0, stream, g);
+}
+
+template <int NT, int MI, int PRO>
+void launch_dec(const DecodeGroup &g, int S, dim3 grid, hipStream_t stream) {
+    switch (S) {
+        case 1: launch_dec_s<NT, MI, PRO, 1>(g, grid, stream); break;
+        case 2: launch_dec_s<NT, MI, PRO, 2>(g, grid, stream); break;
+        case 3: launch_dec_s<NT, MI, PRO, 3>(g, grid, stream); break;
+        case 4: launch_dec_s<NT, MI, PRO, 4>(g, grid, stream); break;
+        case 6: launch_dec_s<NT, MI, PRO, 6>(g, grid, stream); break;
+        default: launch_dec_s<NT, MI, PRO, 10>(g, grid, stream); break;
     }
-    const dim3 grid(max_slices, count), block(kDecThreads);
-    if (ps[0].silu_pair) hipLaunchKernelGGL(gemm_decode_kernel<2>, grid, block, 0, stream, g);
-    else hipLaunchKernelGGL(gemm_decode_kernel<1>, grid, block, 0, stream, g);
+}
+
+// Smallest instantiated S >= min(steps per wave, cap).
+int pick_steps(int spw, int cap) {
+    const int want = std::min(spw, cap);
+    for (int s : {1, 2, 3, 4, 6, 10})
+        if (s >= want && s <= cap) return s;
+    return cap;
+}
+
+int dec_prologue(const GemmParams &p) { return p.ln_gamma ? (p.a_gate ? 2 : 1) : 0; }
+
+// Decode products (M <= 64, K % 4 == 0): one launch per group; all products of
+// a group share the SiLU-pair flag and the prologue kind.
+hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
+    if (count < 1 || count > kMaxDecode) return hipErrorInvalidValue;
+    const int NT = ps[0].silu_pair ? 2 : 1, PRO = dec_prologue(ps[0]);
+    int units1 = 0, spw = 1;
+    for (int i = 0; i < count; ++i) {
+        const GemmParams &p = ps[i];
+        const int slices = p.silu_pair ? p.N / 32 : (p.N + 15) / 16;
+        units1 += slices * ((p.M + 15) / 16);
+        spw = std::max(spw, ((p.K + 15) / 16 + kDecWaves - 1) / kDecWaves);
+    }
+    // Wide products (the LM head) already fill the chip with 64-row tiles.
+    const int MI = (units1 > 1024 && PRO < 2 && !(PRO == 1 && NT == 2)) ? 4 : 1;
+    DecodeGroup g{};
+    g.count = count;
+    for (int i = 0; i < count; ++i) {
+        const GemmParams &p = ps[i];
+        const int slices = p.silu_pair ? p.N / 32 : (p.N + 15) / 16;
+        g.p[i] = p;
+        g.mtiles[i] = (p.M + 16 * MI - 1) / (16 * MI);
+        g.units += slices * g.mtiles[i];
+        g.unit_end[i] = g.units;
+    }
+    g.per_xcd = (g.units + kXcds - 1) / kXcds;
+    const dim3 grid(g.per_xcd * kXcds);
+    const int cap = dec_cap(NT, MI, PRO);
+    const int S = pick_steps(spw, cap);
+    if (PRO == 0) {
+        if (NT == 1) {
+            if (MI == 1) launch_dec<1, 1, 0>(g, S, grid, stream);
+            else launch_dec<1, 4, 0>(g, S, grid, stream);
+        } else {
+            if (MI == 1) launch_dec<2, 1, 0>(g, S, grid, stream);
+            else launch_dec<2, 4, 0>(g, S, grid, stream);
+        }
+    } else if (PRO == 1) {
+        if (NT == 2) launch_dec<2, 1, 1>(g, S, grid, stream);
+        else if (MI == 1) launch_dec<1, 1, 1>(g, S, grid, stream);
+        else launch_dec<1, 4, 1>(g, S, grid, stream);
+    } else {
+        if (NT == 2) return hipErrorInvalidValue;
+        launch_dec<1, 1, 2>(g, S, grid, stream);
+    }
     return hipGetLastError();
 }
 
 bool decode_ok(const GemmParams &p) { return p.M <= 64 && p.K % 4 == 0; }
+
+// The A-side prologue exists on the decode path only, for K <= 1024.
+bool prologue_ok(const GemmParams &p) {
+    if (!p.ln_gamma && !p.a_gate) return true;
+    return p.ln_gamma && p.ln_beta && decode_ok(p) && p.K <= 64 * kDecLnPerLane && !(p.a_gate && p.silu_pair) &&
+           (!p.a_gate || p.ldg >= p.K);
+}
 
 int skinny_splits(int N, int K) {
     const int wave_tiles = (N + 63) / 64;
@@ -722,6 +888,7 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
     // Buffer descriptors address at most 2^31 bytes per 128-row panel.
     if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
+    if (!prologue_ok(p)) return hipErrorInvalidValue;
     if (decode_ok(p)) return launch_decode(&p, 1, stream);
     if (p.M <= 64) {
         int splits = skinny_splits(p.N, p.K);
@@ -743,18 +910,21 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
 
 hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream) {
     if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
+    for (int i = 0; i < count; ++i)
+        if (ps[i].M > 0 && ps[i].N > 0 && !prologue_ok(ps[i])) return hipErrorInvalidValue;
     {
-        // Decode-shaped products: grouped by the SiLU flag into one launch each.
-        GemmParams dec[2][kMaxGroup];
-        int nd[2] = {0, 0};
+        // Decode-shaped products: one launch per (SiLU flag, prologue kind).
+        GemmParams dec[6][kMaxGroup];
+        int nd[6] = {0, 0, 0, 0, 0, 0};
         for (int i = 0; i < count; ++i) {
             const GemmParams &p = ps[i];
             if (p.M <= 0 || p.N <= 0 || !decode_ok(p)) continue;
             if (p.K <= 0 || p.lda < p.K || p.ldw < p.K) return hipErrorInvalidValue;
             if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
-            dec[p.silu_pair ? 1 : 0][nd[p.silu_pair ? 1 : 0]++] = p;
+            const int key = (p.silu_pair ? 3 : 0) + dec_prologue(p);
+            dec[key][nd[key]++] = p;
         }
-        for (int f = 0; f < 2; ++f)
+        for (int f = 0; f < 6; ++f)
             if (nd[f] > 0) {
                 hipError_t e = launch_decode(dec[f], nd[f], stream);
                 if (e != hipSuccess) return e;

@@ -73,10 +73,18 @@ struct GemmParams {
     // `workspace_floats` floats of device memory; nullptr disables splitting.
     float *workspace = nullptr;
     size_t workspace_floats = 0;
+    // Optional A-side prologue (M <= 64, K % 4 == 0, K <= 1024 only): each A row
+    // is replaced by LayerNorm(row) * ln_gamma + ln_beta over its K columns
+    // (eps 1e-5), then multiplied elementwise by a_gate (row stride ldg) if set.
+    const float *ln_gamma = nullptr;
+    const float *ln_beta = nullptr;
+    const float *a_gate = nullptr;
+    int ldg = 0;
 };
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
-// Up to kMaxGroup independent products in one launch (same path: M > 64).
-constexpr int kMaxGroup = 4;
+// Up to kMaxGroup independent products in one launch (M > 64: one launch for
+// the group; M <= 64: one launch per SiLU flag and prologue kind).
+constexpr int kMaxGroup = 6;
 hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream);
 // Workspace the short-M path can use for an N-column product (floats).
 size_t gemm_workspace_floats(int N, int K);
@@ -93,6 +101,10 @@ hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, co
 hipError_t launch_token_shift(const float *x, int Bn, int T, int d, const float *prev_state,
                               const int *slot, const float *mix6, float *out6, size_t out_stride,
                               hipStream_t stream);
+// T = 1 fusion of layernorm -> token_shift -> save_prev: out6 from the normed
+// rows and prev_state[slot[b]] <- LayerNorm(x[b]); d <= 1024.
+hipError_t launch_ln_shift(const float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
+                           const int *slot, const float *mix6, float *out6, size_t out_stride, hipStream_t stream);
 // prev_state[slot[b]] = x[b, T - 1, :]
 hipError_t launch_save_prev(const float *x, int Bn, int T, int d, float *prev_state, const int *slot,
                             hipStream_t stream);

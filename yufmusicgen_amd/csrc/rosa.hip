@@ -320,8 +320,98 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
 
 }  // namespace
 
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    // xor butterfly: both lanes of every pair add the same two values, so all
+    // lanes end with the same bits.
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+}
+
+// Single-token step (T = 1, decode): one wave per stream, EPL channels per
+// lane, the direct recurrence with its two projections (u.m_{t-1} and u.m_t)
+// summed in double across the wave, and the gates computed from the raw
+// pre-activations in place (the same float expressions as the scan's
+// activation path) -- one kernel, no separate gate pass.
+template <int EPL>
+__global__ void __launch_bounds__(256) rosa_step_kernel(RosaParams p) {
+    const int bb = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (bb >= p.B) return;
+    const int D = p.D;
+    const int slot = p.slot ? p.slot[bb] : bb;
+    const bool prepared = p.e_pre != nullptr;
+    const bool gated = p.read_raw != nullptr || prepared;
+    const size_t base = (size_t)bb * p.ld;
+    float u[EPL], lam[EPL], m[EPL], ev[EPL], gv[EPL];
+    float nrm = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int c = lane + e * kWave;
+        const bool ok = c < D;
+        u[e] = ok ? p.direction[c] : 0.0f;
+        lam[e] = ok ? p.decay[c] : 0.0f;
+        m[e] = (ok && p.memory_in) ? p.memory_in[(size_t)slot * D + c] : 0.0f;
+        ev[e] = ok ? (prepared ? p.e_pre : p.cand)[base + c] : 0.0f;
+        gv[e] = ok ? (prepared ? p.g_pre : p.write)[base + c] : 0.0f;
+        nrm = fmaf(u[e], u[e], nrm);
+    }
+    float rr[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int c = lane + e * kWave;
+        rr[e] = (c < D && gated && !prepared) ? p.read_raw[base + c] : 0.0f;
+    }
+    if (p.raw_params) {
+        const float inv = 1.0f / fmaxf(sqrtf(wave_sum(nrm)), 1e-12f);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int c = lane + e * kWave;
+            u[e] *= inv;
+            lam[e] = c < D ? 1.0f / (1.0f + expf(-lam[e])) : 0.0f;
+        }
+    }
+    if (!prepared) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * ev[e]) + 1.0f);
+            ev[e] = th * __frcp_rn(1.0f + __expf(-gv[e]));
+            gv[e] = gated ? __frcp_rn(1.0f + __expf(-rr[e])) : 1.0f;
+        }
+    }
+    double f = 0.0;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) f = fma((double)u[e], (double)m[e], f);
+    const float p1 = (float)wave_sum_f64(f);
+    double f2 = 0.0;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        m[e] = fmaf(lam[e], fmaf(-2.0f * p1, u[e], m[e]), ev[e]);
+        f2 = fma((double)u[e], (double)m[e], f2);
+    }
+    const float p2 = (float)wave_sum_f64(f2);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int c = lane + e * kWave;
+        if (c < D) {
+            p.read_out[(size_t)bb * D + c] = fmaf(-2.0f * p2, u[e], m[e]) * gv[e];
+            if (p.memory_out) p.memory_out[(size_t)slot * D + c] = m[e];
+        }
+    }
+}
+
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
     if (p.B <= 0) return hipSuccess;
+    if (p.T == 1) {
+        const dim3 grid((p.B + 3) / 4), block(256);
+        const int epl = (p.D + kWave - 1) / kWave;
+        if (epl <= 1) hipLaunchKernelGGL(rosa_step_kernel<1>, grid, block, 0, stream, p);
+        else if (epl <= 2) hipLaunchKernelGGL(rosa_step_kernel<2>, grid, block, 0, stream, p);
+        else if (epl <= 4) hipLaunchKernelGGL(rosa_step_kernel<4>, grid, block, 0, stream, p);
+        else if (epl <= 8) hipLaunchKernelGGL(rosa_step_kernel<8>, grid, block, 0, stream, p);
+        else if (epl <= 16) hipLaunchKernelGGL(rosa_step_kernel<16>, grid, block, 0, stream, p);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     const dim3 grid(p.B), block(kThreads);
     const int epl = (p.D + kWave - 1) / kWave;
     if (epl <= 1) hipLaunchKernelGGL(rosa_scan_kernel<1>, grid, block, 0, stream, p);

@@ -306,8 +306,111 @@ __global__ void __launch_bounds__(kWave) wkv7_scan_kernel(WkvParams p, int waves
     }
 }
 
+// Single-token step (T = 1, decode): the same lane layout as the scan (L lanes
+// per state row, E columns per lane, R rows per wave), but with no LDS staging:
+// every lane loads its E columns of r, w, k, a (b), k_k, k_a and its rows' v
+// and state straight from global memory, all issued before the first use, so a
+// step costs one memory round trip.  The per-head L2 norm of k * k_k is an
+// L-lane butterfly (each row's L lanes cover all N columns), as are S a and
+// S r.  Four waves per workgroup, B * H * W waves in all.
+template <int N, bool PREP>
+__global__ void __launch_bounds__(256) wkv7_step_kernel(WkvParams p, int waves_total) {
+    using Lay = Layout<N>;
+    constexpr int E = Lay::E, L = Lay::L, R = Lay::R, W = Lay::W;
+    const int flat = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (flat >= waves_total) return;
+    const int lane = threadIdx.x & 63;
+    const int head = flat / W, wave = flat - head * W;
+    const int bb = head / p.H, h = head - bb * p.H;
+    const int rl = lane / L, cl = lane - rl * L;
+    const int i = wave * R + rl, j0 = cl * E;
+    const bool row_ok = i < N;
+    const int slot = p.slot ? p.slot[bb] : bb;
+    const size_t state_off = ((size_t)slot * p.H + h) * N * N;
+    const size_t base = ((size_t)bb * p.H + h) * N;  // token (bb, 0)
+
+    const auto rs = make_rsrc(p.state_in ? p.state_in + state_off : nullptr, p.state_in ? N * N * 4 : 0u);
+    const auto rr = make_rsrc(p.r + base, N * 4), rw = make_rsrc(p.w + base, N * 4);
+    const auto rk = make_rsrc(p.k + base, N * 4), ra = make_rsrc(p.a + base, N * 4);
+    const auto rb = make_rsrc(PREP ? nullptr : p.b + base, PREP ? 0u : N * 4);
+    const auto rkk = make_rsrc(PREP ? p.k_k + h * N : nullptr, PREP ? N * 4 : 0u);
+    const auto rka = make_rsrc(PREP ? p.k_a + h * N : nullptr, PREP ? N * 4 : 0u);
+    float s[E], rv[E], wv[E], kv[E], av[E], bv[E], kk[E], ka[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const uint32_t off = (uint32_t)(j0 + e) * 4u;
+        s[e] = buf_load(rs, row_ok ? (uint32_t)(i * N + j0 + e) * 4u : kBufferOob);
+        rv[e] = buf_load(rr, off);
+        wv[e] = buf_load(rw, off);
+        kv[e] = buf_load(rk, off);
+        av[e] = buf_load(ra, off);
+        if constexpr (PREP) {
+            kk[e] = buf_load(rkk, off);
+            ka[e] = buf_load(rka, off);
+        } else {
+            bv[e] = buf_load(rb, off);
+        }
+    }
+    const float vi = buf_load(make_rsrc(p.v + base, N * 4), row_ok ? (uint32_t)i * 4u : kBufferOob);
+
+    float dv[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        // d = exp(-e^{-0.5} sigmoid(w)) = exp2(-e^{-0.5} log2(e) sigmoid(w)).
+        const float sig = __frcp_rn(1.0f + __expf(-wv[e]));
+        dv[e] = exp2f(-0.8750387749f * sig);
+    }
+    if constexpr (PREP) {
+        // kappa = normalize(k * k_k) over the head (F.normalize, eps 1e-12).
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float x = kv[e] * kk[e];
+            sq = fmaf(x, x, sq);
+        }
+        const float inv = 1.0f / fmaxf(sqrtf(group_sum<L>(sq)), 1e-12f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const float kap = kv[e] * kk[e] * inv;
+            const float alpha = av[e];
+            av[e] = -kap;
+            bv[e] = kap * alpha;
+            kv[e] = kv[e] * (1.0f + (alpha - 1.0f) * ka[e]);
+        }
+    }
+    float sa = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) sa = fmaf(s[e], av[e], sa);
+    sa = group_sum<L>(sa);
+    float yv = 0.0f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        s[e] = fmaf(s[e], dv[e], fmaf(sa, bv[e], kv[e] * vi));
+        yv = fmaf(s[e], rv[e], yv);
+    }
+    yv = group_sum<L>(yv);
+    if (row_ok && cl == 0) p.y[base + i] = yv;
+    if (p.state_out && row_ok) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) p.state_out[state_off + (size_t)i * N + j0 + e] = s[e];
+    }
+}
+
+template <int N>
+hipError_t launch_step_n(const WkvParams &p, bool prep, hipStream_t stream) {
+    using Lay = Layout<N>;
+    const int waves = p.B * p.H * Lay::W;
+    const dim3 grid((waves + 3) / 4), block(256);
+    if (prep)
+        hipLaunchKernelGGL((wkv7_step_kernel<N, true>), grid, block, 0, stream, p, waves);
+    else
+        hipLaunchKernelGGL((wkv7_step_kernel<N, false>), grid, block, 0, stream, p, waves);
+    return hipGetLastError();
+}
+
 template <int N>
 hipError_t launch_n(const WkvParams &p, bool prep, hipStream_t stream) {
+    if (p.T == 1) return launch_step_n<N>(p, prep, stream);
     using Lay = Layout<N>;
     const int waves = p.B * p.H * Lay::W;
     const int per_xcd = (waves + kXcds - 1) / kXcds;
