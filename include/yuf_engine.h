@@ -105,6 +105,21 @@ int yuf_rosa_scan_f32(int B, int T, int D,
 int yuf_linear_f32(int M, int N, int K, const float *A, const float *W, const float *bias, int act,
                    const float *residual, float *C, void *stream);
 
+/*
+ * LayerNorm -> (gate) -> Linear in one kernel, for short products (M <= 64, the
+ * decode shapes): C = (LayerNorm(A) * gamma + beta) [* gate] W^T + bias + residual.
+ * The norm -> projection pairs of a block: out_norm(y) * g -> output
+ * (yufmusicgen/model.py:195-196), the ROSA and FFN pre-norms
+ * (model.py:306, :377), the final norm -> LM head (model.py:390-391).
+ * LayerNorm over the K columns of each A row, eps 1e-5 (torch.nn.LayerNorm).
+ *   A [M, K], gate [M, K] or NULL, gamma / beta [K], W [N, K], C [M, N];
+ *   bias [N] or NULL; residual [M, N] or NULL (may alias C).
+ * Requires 1 <= M <= 64, K % 4 == 0, K <= 1024 (else YUF_ERR_INVALID).
+ */
+int yuf_ln_linear_f32(int M, int N, int K, const float *A, const float *gamma, const float *beta,
+                      const float *gate, const float *W, const float *bias, const float *residual, float *C,
+                      void *stream);
+
 /* ---------------------------------------------------------------------------
  * Checkpoints (.yuf).  Replaces `Checkpoint::load / tensor / tensor_dims`
  * (vulkan/src/checkpoint.rs:90-176).

@@ -201,6 +201,32 @@ def test_device_sampling():
     assert float((emp - p).abs().sum()) < 0.5
 
 
+def test_device_sampling_ties():
+    """Ties at the k-th value: lower token ids win on the pooled path; with more
+    than 1024 logits at the selection bound the radix fallback is taken."""
+    V, k = 20480, 32
+    torch.manual_seed(1)
+    # Row 0: 40 equal top logits -> the top 32 are the 32 lowest of those ids.
+    # Row 1: five logits of 1.0 over a sea of zeros (every logit passes the
+    # bound: radix path); a cold temperature puts the draw on the five.
+    logits = torch.randn(2, V, device="cuda")
+    ids0 = torch.randperm(V)[:40].sort().values
+    logits[0, ids0.cuda()] = 10.0
+    logits[1] = 0.0
+    ids1 = torch.tensor([7, 300, 4096, 9999, 20479])
+    logits[1, ids1.cuda()] = 1.0
+    tokens = torch.empty(2, dtype=torch.int32, device="cuda")
+    seen0 = set()
+    for c in range(64):
+        sample_device(logits, tokens, 0.05, k, seed=5, counter=c)
+        torch.cuda.synchronize()
+        t0, t1 = int(tokens[0]), int(tokens[1])
+        assert t0 in set(ids0[:k].tolist()), t0
+        assert t1 in set(ids1.tolist()), t1
+        seen0.add(t0)
+    assert len(seen0) > 8  # the 32 tied logits are drawn uniformly
+
+
 @pytest.mark.parametrize("preset,branches", [("tiny", 1), ("tiny", 2), ("tiny", 3), ("0.1b", 2), ("0.1b", 4)])
 def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, preset, branches):
     """Decode steps replayed from the captured HIP graph equal eager steps

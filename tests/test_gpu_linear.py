@@ -52,3 +52,43 @@ def test_linear_epilogues(act, m, n):
     z = a.astype(np.float64) @ w.astype(np.float64).T + bias
     z = {0: z, 1: np.tanh(z), 2: 1.0 / (1.0 + np.exp(-z))}[act] + res
     np.testing.assert_allclose(run_linear(a, w, bias, act, res), z, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("m,n,k,gated", [(64, 640, 640, False), (64, 640, 640, True), (37, 384, 640, False),
+                                         (5, 100, 36, True), (64, 1280, 1024, False), (64, 640, 1024, True),
+                                         (64, 9000, 640, False), (20, 48, 1024, True)])
+def test_ln_linear_matches_float64(m, n, k, gated):
+    """LayerNorm (-> gate) -> Linear in one decode kernel.  K = 1024 with a gate,
+    and the 9000-wide product (64-row tiles), take the statistics pass that
+    re-reads the rows; the others reuse the A values already loaded."""
+    print(f"ln_linear {m}x{n}x{k} gate={gated}", flush=True)
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = (rng.standard_normal((m, k)) * 2.0 + 0.5).astype(np.float32)
+    gamma = (1.0 + 0.1 * rng.standard_normal(k)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(k)).astype(np.float32)
+    gate = rng.uniform(0.0, 1.0, (m, k)).astype(np.float32) if gated else None
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    a64 = a.astype(np.float64)
+    xn = (a64 - a64.mean(1, keepdims=True)) / np.sqrt(a64.var(1, keepdims=True) + 1e-5) * gamma + beta
+    if gated:
+        xn = xn * gate
+    expect = xn @ w.astype(np.float64).T + bias + res
+    dev = {name: torch.from_numpy(x).cuda() for name, x in
+           dict(a=a, gamma=gamma, beta=beta, w=w, bias=bias, res=res).items()}
+    G = torch.from_numpy(gate).cuda() if gated else None
+    C = torch.empty(m, n, device="cuda")
+    check(lib().yuf_ln_linear_f32(m, n, k, dev["a"].data_ptr(), dev["gamma"].data_ptr(), dev["beta"].data_ptr(),
+                                  None if G is None else G.data_ptr(), dev["w"].data_ptr(), dev["bias"].data_ptr(),
+                                  dev["res"].data_ptr(), C.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(C.cpu().numpy(), expect, rtol=1e-4, atol=2e-4 * np.sqrt(k) * 0.05)
+
+
+def test_ln_linear_rejects_long_batches():
+    from yufmusicgen_amd._lib import YufError
+    A = torch.zeros(65, 64, device="cuda")
+    with pytest.raises(YufError):
+        check(lib().yuf_ln_linear_f32(65, 8, 64, A.data_ptr(), A.data_ptr(), A.data_ptr(), None, A.data_ptr(), None,
+                                      None, A.data_ptr(), None))

@@ -46,6 +46,7 @@ SIGNATURES = {
     "yuf_wkv7_scan_f32": (ctypes.c_int, [ctypes.c_int] * 4 + [c_void_p] * 10),
     "yuf_rosa_scan_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
+    "yuf_ln_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_ckpt_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),
     "yuf_ckpt_free": (None, [c_void_p]),
     "yuf_ckpt_config": (ctypes.c_int, [c_void_p, ctypes.POINTER(ModelConfigC)]),

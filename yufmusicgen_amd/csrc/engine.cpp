@@ -78,20 +78,21 @@ struct Engine {
     // buffers change.
     // YUF_NO_GRAPH=1 runs every step eagerly.
     bool use_graphs = true;
-    hipGraphExec_t step_exec = nullptr;
+    hipGraphExec_t step_exec[5] = {};  // one per branch + the LM head (one graph when unbranched)
     int step_n = 0;
     const int32_t *step_tok = nullptr;
     float *step_logits = nullptr;
-    // The captured step splits its streams into `branches` groups recorded on
-    // their own HIP streams (fork / join events): independent chains of small
-    // kernels that the GPU overlaps.  YUF_DECODE_BRANCHES=1..4 overrides.
+    // The step can split its streams into `branches` groups replayed on their
+    // own HIP streams (fork / join events): independent chains of small
+    // kernels that the hardware queues overlap.  YUF_DECODE_BRANCHES=1..4.
     static constexpr int kMaxBranches = 4;
     int branches = 1;
     hipStream_t side[kMaxBranches - 1] = {};
     hipEvent_t fork = nullptr, join[kMaxBranches - 1] = {};
 
     ~Engine() {
-        if (step_exec) (void)hipGraphExecDestroy(step_exec);
+        for (auto g : step_exec)
+            if (g) (void)hipGraphExecDestroy(g);
         for (int i = 0; i < kMaxBranches - 1; ++i) {
             if (side[i]) (void)hipStreamDestroy(side[i]);
             if (join[i]) (void)hipEventDestroy(join[i]);
@@ -462,60 +463,91 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
     return YUF_OK;
 }
 
-// One decode step (T = 1, last-position logits) of n streams whose slots are
-// already on the device, replayed from a captured graph when possible.  The
-// captured work is kernels and one device-to-device copy only (no memset
-// nodes, no host synchronisation).
-// The work of one captured step: the token copy on the engine stream, then the
-// layers of each group of streams, group 0 on the engine stream and the others
-// on side streams forked from and joined back into it, then the final norm and
-// LM head once for all n streams (the head's weights are read once per step).
-int step_record(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
-    ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice, e.stream),
-            "tokens copy");
-    const int G = std::max(1, std::min(e.branches, n));
-    if (G == 1) return forward_pass(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev, YUF_LOGITS_LAST, 1, 0);
-    ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
-    for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.side[g - 1], e.fork, 0), "fork wait");
-    for (int g = 0; g < G; ++g) {
-        const int s0 = (int)((long long)n * g / G), s1 = (int)((long long)n * (g + 1) / G);
-        hipStream_t st = g == 0 ? e.stream : e.side[g - 1];
-        const int rc = forward_pass(e, act_at(e, st, s0, 1), s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
-        if (rc != YUF_OK) return rc;
+// Capture `body` (launches on stream st) into an executable graph.
+template <typename F>
+int capture(hipStream_t st, F &&body, hipGraphExec_t *out) {
+    ENG_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "capture begin");
+    const int rc = body();
+    hipGraph_t graph = nullptr;
+    const hipError_t ce = hipStreamEndCapture(st, &graph);
+    if (rc != YUF_OK || ce != hipSuccess) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc != YUF_OK ? rc : hip_fail(ce, "capture end");
     }
-    for (int g = 1; g < G; ++g) {
-        ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
-        ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+    const hipError_t ie = hipGraphInstantiate(out, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    if (ie != hipSuccess) {
+        *out = nullptr;
+        return hip_fail(ie, "graph instantiate");
     }
-    return lm_head_last(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev);
+    return YUF_OK;
 }
 
+int drop_step_graphs(Engine &e) {
+    for (auto &g : e.step_exec)
+        if (g) {
+            ENG_TRY(hipGraphExecDestroy(g), "graph destroy");
+            g = nullptr;
+        }
+    return YUF_OK;
+}
+
+// One decode step (T = 1, last-position logits) of n streams whose slots are
+// already on the device, replayed from captured graphs (kernels and one
+// device-to-device copy only: no memset nodes, no host synchronisation).
+// With one branch the whole step is one graph.  With G > 1 the streams are
+// split into G groups whose layers are G graphs launched on G HIP streams
+// (forked from and joined back into the engine stream with events, so the
+// hardware queues run them side by side), then one graph with the final norm
+// and the LM head over all n streams (its weights are read once per step).
 int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
     if (!e.use_graphs) return prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
-    if (!(e.step_exec && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
-        if (e.step_exec) {
-            ENG_TRY(hipGraphExecDestroy(e.step_exec), "graph destroy");
-            e.step_exec = nullptr;
+    const int G = std::max(1, std::min(e.branches, n));
+    auto group = [&](int g) { return std::make_pair((int)((long long)n * g / G), (int)((long long)n * (g + 1) / G)); };
+    auto stream_of = [&](int g) { return g == 0 ? e.stream : e.side[g - 1]; };
+    if (!(e.step_exec[0] && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
+        int rc = drop_step_graphs(e);
+        if (rc != YUF_OK) return rc;
+        if (G == 1) {
+            rc = capture(e.stream, [&]() {
+                ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice,
+                                       e.stream), "tokens copy");
+                return forward_pass(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev, YUF_LOGITS_LAST, 1, 0);
+            }, &e.step_exec[0]);
+        } else {
+            for (int g = 0; g < G && rc == YUF_OK; ++g) {
+                const auto [s0, s1] = group(g);
+                hipStream_t st = stream_of(g);
+                rc = capture(st, [&]() {
+                    return forward_pass(e, act_at(e, st, s0, 1), s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
+                }, &e.step_exec[g]);
+            }
+            if (rc == YUF_OK)
+                rc = capture(e.stream, [&]() { return lm_head_last(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev); },
+                             &e.step_exec[G]);
         }
-        ENG_TRY(hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal), "capture begin");
-        const int rc = step_record(e, n, tokens_dev, logits_dev);
-        hipGraph_t graph = nullptr;
-        const hipError_t ce = hipStreamEndCapture(e.stream, &graph);
-        if (rc != YUF_OK || ce != hipSuccess) {
-            if (graph) (void)hipGraphDestroy(graph);
-            return rc != YUF_OK ? rc : hip_fail(ce, "capture end");
-        }
-        const hipError_t ie = hipGraphInstantiate(&e.step_exec, graph, nullptr, nullptr, 0);
-        (void)hipGraphDestroy(graph);
-        if (ie != hipSuccess) {
-            e.step_exec = nullptr;
-            return hip_fail(ie, "graph instantiate");
+        if (rc != YUF_OK) {
+            (void)drop_step_graphs(e);
+            return rc;
         }
         e.step_n = n;
         e.step_tok = tokens_dev;
         e.step_logits = logits_dev;
     }
-    ENG_TRY(hipGraphLaunch(e.step_exec, e.stream), "graph launch");
+    if (G == 1) {
+        ENG_TRY(hipGraphLaunch(e.step_exec[0], e.stream), "graph launch");
+        return YUF_OK;
+    }
+    ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice, e.stream),
+            "tokens copy");
+    ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
+    for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.side[g - 1], e.fork, 0), "fork wait");
+    for (int g = 0; g < G; ++g) ENG_TRY(hipGraphLaunch(e.step_exec[g], stream_of(g)), "graph launch");
+    for (int g = 1; g < G; ++g) {
+        ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
+        ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+    }
+    ENG_TRY(hipGraphLaunch(e.step_exec[G], e.stream), "graph launch");
     return YUF_OK;
 }
 

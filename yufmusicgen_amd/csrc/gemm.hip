@@ -460,27 +460,34 @@ constexpr int dec_cap(int NT, int MI, int PRO) {
     return MI == 1 ? (NT == 1 && PRO < 2 ? 10 : 6) : (NT == 1 ? (PRO == 0 ? 4 : 3) : 3);
 }
 
-template <int NT, int MI, int S, int PRO>
+// MULTI = false: a single product, whose parameters sit at fixed kernel-argument
+// offsets (no dependent argument load to find the product of a unit).
+template <int NT, int MI, int S, int PRO, bool MULTI>
 __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g) {
     constexpr int RT = 16 * MI;  // rows per workgroup
     __shared__ __attribute__((aligned(16))) float red[kDecWaves][NT][RT * 17];
     __shared__ float stats[PRO > 0 ? RT : 1][2];
+    __shared__ float part[2][PRO > 0 ? kDecWaves : 1][PRO > 0 ? RT : 1];  // per-wave row partial sums
     __shared__ __attribute__((aligned(16))) float affine[PRO > 0 ? 2 * 64 * kDecLnPerLane : 4];  // gamma | beta
 
     const int u = (blockIdx.x % kXcds) * g.per_xcd + blockIdx.x / kXcds;
     if (u >= g.units) return;
     int pi = 0;
+    if constexpr (MULTI) {
 #pragma unroll
-    for (int i = 1; i < kMaxDecode; ++i) pi += (i < g.count && u >= g.unit_end[i - 1]) ? 1 : 0;
-    const GemmParams &p = g.p[pi];
-    const int local = u - (pi > 0 ? g.unit_end[pi - 1] : 0);
-    const int slice = local / g.mtiles[pi], mt = local - slice * g.mtiles[pi];
+        for (int i = 1; i < kMaxDecode; ++i) pi += (i < g.count && u >= g.unit_end[i - 1]) ? 1 : 0;
+    }
+    const GemmParams &p = g.p[MULTI ? pi : 0];
+    const int local = MULTI && pi > 0 ? u - g.unit_end[pi - 1] : u;
+    const int mtiles = g.mtiles[MULTI ? pi : 0];
+    const int slice = local / mtiles, mt = local - slice * mtiles;
     // NT = 1 -> 16 consecutive W rows; NT = 2 (SiLU pair) -> rows c and c + 32
     // of one 64-row [in | gate] block.
     const int w_row0 = NT == 1 ? slice * 16 : (slice / 2) * 64 + (slice % 2) * 16;
     const int row0 = mt * RT;
     const int rows = min(p.M - row0, RT);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: k ranges and step guards are scalar
     const int g4 = lane >> 4, li = lane & 15;
     const int spw = ((p.K + 15) / 16 + kDecWaves - 1) / kDecWaves;  // 16-k steps per wave
     const int k_begin = min(p.K, wave * spw * 16), k_end = min(p.K, k_begin + spw * 16);
@@ -528,41 +535,89 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
             affine[c] = p.ln_gamma[c];
             affine[64 * kDecLnPerLane + c] = p.ln_beta[c];
         }
-        // Row statistics: wave w normalises rows w, w + 16, ... of the tile.
-        for (int rr = wave; rr < RT; rr += kDecWaves) {
-            float v[kDecLnPerLane];
-            float sum = 0.0f;
+        if (spw <= S) {
+            // One round covers this wave's K range, so the row statistics come
+            // from the A values already in registers: per-wave partial sums over
+            // the wave's columns, combined across the waves through LDS (two
+            // passes: the mean, then the squared deviations from it).
+            float ps[MI];
 #pragma unroll
-            for (int e = 0; e < kDecLnPerLane; ++e) {
-                const int c = lane + e * 64;
-                v[e] = buf_load(ra, c < p.K ? (uint32_t)((size_t)rr * p.lda + c) * 4u : kBufferOob);
-                sum += v[e];
-            }
-            const float mu = wave_sum(sum) / (float)p.K;
-            float sq = 0.0f;
+            for (int i = 0; i < MI; ++i) {
+                ps[i] = 0.0f;
 #pragma unroll
-            for (int e = 0; e < kDecLnPerLane; ++e) {
-                const int c = lane + e * 64;
-                const float dv = c < p.K ? v[e] - mu : 0.0f;
-                sq = fmaf(dv, dv, sq);
+                for (int s = 0; s < S; ++s) ps[i] += (a[s][i][0] + a[s][i][1]) + (a[s][i][2] + a[s][i][3]);
+                ps[i] += __shfl_xor(ps[i], 16);
+                ps[i] += __shfl_xor(ps[i], 32);
+                if (g4 == 0) part[0][wave][16 * i + li] = ps[i];
             }
-            const float rs = rsqrtf(wave_sum(sq) / (float)p.K + 1e-5f);
-            if (lane == 0) {
-                stats[rr][0] = mu;
-                stats[rr][1] = rs;
-            }
-        }
-        lds_barrier();
+            lds_barrier();
 #pragma unroll
-        for (int i = 0; i < MI; ++i) {
-            mean[i] = stats[16 * i + li][0];
-            rstd[i] = stats[16 * i + li][1];
+            for (int i = 0; i < MI; ++i) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kDecWaves; ++w) sum += part[0][w][16 * i + li];
+                mean[i] = sum / (float)p.K;
+                float sq = 0.0f;
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    if (k_begin + 16 * s + 4 * g4 < k_end) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float dv = a[s][i][q] - mean[i];
+                            sq = fmaf(dv, dv, sq);
+                        }
+                    }
+                }
+                sq += __shfl_xor(sq, 16);
+                sq += __shfl_xor(sq, 32);
+                if (g4 == 0) part[1][wave][16 * i + li] = sq;
+            }
+            lds_barrier();
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                float sq = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kDecWaves; ++w) sq += part[1][w][16 * i + li];
+                rstd[i] = rsqrtf(sq / (float)p.K + 1e-5f);
+            }
+        } else {
+            // Row statistics: wave w normalises rows w, w + 16, ... of the tile.
+            for (int rr = wave; rr < RT; rr += kDecWaves) {
+                float v[kDecLnPerLane];
+                float sum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < kDecLnPerLane; ++e) {
+                    const int c = lane + e * 64;
+                    v[e] = buf_load(ra, c < p.K ? (uint32_t)((size_t)rr * p.lda + c) * 4u : kBufferOob);
+                    sum += v[e];
+                }
+                const float mu = wave_sum(sum) / (float)p.K;
+                float sq = 0.0f;
+#pragma unroll
+                for (int e = 0; e < kDecLnPerLane; ++e) {
+                    const int c = lane + e * 64;
+                    const float dv = c < p.K ? v[e] - mu : 0.0f;
+                    sq = fmaf(dv, dv, sq);
+                }
+                const float rs = rsqrtf(wave_sum(sq) / (float)p.K + 1e-5f);
+                if (lane == 0) {
+                    stats[rr][0] = mu;
+                    stats[rr][1] = rs;
+                }
+            }
+            lds_barrier();
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                mean[i] = stats[16 * i + li][0];
+                rstd[i] = stats[16 * i + li][1];
+            }
         }
     }
 
     for (int k0 = k_begin;;) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
+            if (k0 + 16 * s >= k_end) break;  // steps past this wave's K range: no MFMAs on zeros
             if constexpr (PRO > 0) {
                 const int k = k0 + 16 * s + 4 * g4;
                 if (k < k_end) {
@@ -790,8 +845,12 @@ void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStre
 
 template <int NT, int MI, int PRO, int S>
 void launch_dec_s(const DecodeGroup &g, dim3 grid, hipStream_t stream) {
-    if constexpr (S <= dec_cap(NT, MI, PRO))
-        hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO>), grid, dim3(kDecThreads), 0, stream, g);
+    if constexpr (S <= dec_cap(NT, MI, PRO)) {
+        if (g.count == 1)
+            hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO, false>), grid, dim3(kDecThreads), 0, stream, g);
+        else if constexpr (PRO == 0)
+            hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO, true>), grid, dim3(kDecThreads), 0, stream, g);
+    }
 }
 
 template <int NT, int MI, int PRO>
@@ -821,6 +880,13 @@ int dec_prologue(const GemmParams &p) { return p.ln_gamma ? (p.a_gate ? 2 : 1) :
 hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
     if (count < 1 || count > kMaxDecode) return hipErrorInvalidValue;
     const int NT = ps[0].silu_pair ? 2 : 1, PRO = dec_prologue(ps[0]);
+    if (PRO > 0 && count > 1) {  // grouped launches exist for plain products only
+        for (int i = 0; i < count; ++i) {
+            const hipError_t e = launch_decode(ps + i, 1, stream);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     int units1 = 0, spw = 1;
     for (int i = 0; i < count; ++i) {
         const GemmParams &p = ps[i];
@@ -1007,5 +1073,21 @@ extern "C" int yuf_linear_f32(int M, int N, int K, const float *A, const float *
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = N;
     hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
     if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("linear launch: ") + hipGetErrorString(err));
+    return YUF_OK;
+}
+
+extern "C" int yuf_ln_linear_f32(int M, int N, int K, const float *A, const float *gamma, const float *beta,
+                                 const float *gate, const float *W, const float *bias, const float *residual, float *C,
+                                 void *stream) {
+    using namespace yuf;
+    if (M < 1 || M > 64 || N < 0 || K < 4 || K % 4 != 0 || K > 1024)
+        return fail(YUF_ERR_INVALID, "ln_linear: needs 1 <= M <= 64, K % 4 == 0, 4 <= K <= 1024");
+    if (N > 0 && (!A || !gamma || !beta || !W || !C)) return fail(YUF_ERR_INVALID, "ln_linear: null pointer");
+    GemmParams p;
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = K; p.W = W; p.ldw = K; p.C = C; p.ldc = N;
+    p.bias = bias; p.residual = residual; p.ldr = N;
+    p.ln_gamma = gamma; p.ln_beta = beta; p.a_gate = gate; p.ldg = gate ? K : 0;
+    hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("ln_linear launch: ") + hipGetErrorString(err));
     return YUF_OK;
 }
