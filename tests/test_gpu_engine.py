@@ -130,11 +130,13 @@ def test_tiny_model_prompt_and_greedy_match_reference(golden_dir, tmp_path):
         np.testing.assert_allclose(last, z["greedy_logits"][i], rtol=0, atol=LOGIT_ATOL)
 
 
-@pytest.mark.parametrize("steps", [80, 160])
+@pytest.mark.parametrize("steps", [80, 160, 256])
 def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path, steps):
     """The 0.1B architecture (14L, d=640, 16x40, ROSA 128, V=20480) on a short
     batch, prefill then decode, against the float64 oracle.  2 x 160 tokens
-    put every prefill product on the 256-row GEMM tiles."""
+    put every prefill product on the 256-row GEMM tiles; 2 x 256 tokens run as
+    two 128-token chunks whose ROSA scans take the segmented path (64-token
+    segments), the second from the carried state."""
     cfg = PRESETS["0.1b"]
     weights = synth_weights(cfg, seed=0)
     path = tmp_path / "m.yuf"
@@ -152,6 +154,27 @@ def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path, steps):
         np.testing.assert_allclose(g, r.numpy(), rtol=0, atol=LOGIT_ATOL)
     blob = _states_from_blob(eng, [0, 1])
     np.testing.assert_allclose(blob, state_to_blob(state), rtol=1e-4, atol=1e-4)
+
+
+def test_rosa_segmented_prefill_matches_sequential(tmp_path, monkeypatch):
+    """The segmented ROSA prefill (parallel 64-token segments around an A^64
+    carry pass) against the sequential chunked scan, through the whole model:
+    logits and states, with a carried state and a decode step after it."""
+    cfg = PRESETS["0.1b"]
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=5))
+    ck = Checkpoint.load(path)
+    tokens = uniform_tokens(9, 3, 320, cfg.vocab_size)
+    outs = []
+    for seg in ("1", "0"):
+        monkeypatch.setenv("YUF_ROSA_SEGMENTED", seg)
+        eng = Engine(ck, max_streams=3, max_tokens=3 * 192)
+        head = eng.prefill(tokens[:, :192], logits="all")
+        tail = eng.prefill(tokens[:, 192:], logits="all")  # 128 tokens from the carried state
+        nxt = eng.step(tokens[:, 0])
+        outs.append((head, tail, nxt, _states_from_blob(eng, [0, 1, 2])))
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-4)
 
 
 def test_wide_decode_batch_vs_oracle(tmp_path):

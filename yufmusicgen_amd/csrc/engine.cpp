@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -41,7 +42,11 @@ struct LayerW {
     const float *ln_o_w, *ln_o_b, *ln_r_w, *ln_r_b;
     const float *rosa_w3, *rosa_b3, *rosa_hh, *rosa_decay, *rosa_out;
     const float *ln_f_w, *ln_f_b, *ffn_cat, *ffn_out;
+    const float *rosa_al;  // A^kRosaSeg of the ROSA transition, [D][D] row-major
 };
+
+// Segment length of the segmented ROSA prefill scan.
+constexpr int kRosaSeg = 64;
 
 struct DeviceBuf {
     void *p = nullptr;
@@ -65,6 +70,8 @@ struct Engine {
     float *h = nullptr, *xn = nullptr, *mix = nullptr, *r = nullptr, *k = nullptr, *v = nullptr, *wr = nullptr,
           *al = nullptr, *g = nullptr, *lr = nullptr, *y = nullptr, *z = nullptr, *rosa3 = nullptr, *rread = nullptr,
           *ffn = nullptr, *hl = nullptr;
+    float *rz = nullptr, *rcarry = nullptr, *rends = nullptr;  // segmented ROSA scratch
+    bool rosa_segmented = true;                                // YUF_ROSA_SEGMENTED=0 disables
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
     size_t gemm_ws_floats = 0;
     int *slots_dev = nullptr, *tokens_dev = nullptr, *bad_dev = nullptr;
@@ -230,6 +237,35 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
             append(cat.data(), cat.size());
         }
         if (!mat("ffn_out.weight", d, hid)) return YUF_ERR_FORMAT;
+        {
+            // A^L for the segmented ROSA scan, A = diag(lambda) (I - 2 u u^T) with
+            // lambda = sigmoid(decay), u = householder / max(|householder|, 1e-12)
+            // (yufmusicgen/model.py:300-301): column j is A applied L times to e_j,
+            // in double precision through the rank-one form A x = lambda (x - 2 (u.x) u).
+            const float *hh = get(pre + "rosa.householder", {D});
+            const float *dec = get(pre + "rosa.decay", {D});
+            if (!hh || !dec) return YUF_ERR_FORMAT;
+            std::vector<double> u((size_t)D), lam((size_t)D), x((size_t)D);
+            double nrm = 0.0;
+            for (long long j = 0; j < D; ++j) nrm += (double)hh[j] * hh[j];
+            nrm = std::max(std::sqrt(nrm), 1e-12);
+            for (long long j = 0; j < D; ++j) {
+                u[(size_t)j] = hh[j] / nrm;
+                lam[(size_t)j] = 1.0 / (1.0 + std::exp(-(double)dec[j]));
+            }
+            std::vector<float> al((size_t)(D * D));
+            for (long long j = 0; j < D; ++j) {
+                std::fill(x.begin(), x.end(), 0.0);
+                x[(size_t)j] = 1.0;
+                for (int step = 0; step < kRosaSeg; ++step) {
+                    double pr = 0.0;
+                    for (long long i = 0; i < D; ++i) pr += u[(size_t)i] * x[(size_t)i];
+                    for (long long i = 0; i < D; ++i) x[(size_t)i] = lam[(size_t)i] * (x[(size_t)i] - 2.0 * pr * u[(size_t)i]);
+                }
+                for (long long i = 0; i < D; ++i) al[(size_t)(i * D + j)] = (float)x[(size_t)i];
+            }
+            append(al.data(), al.size());
+        }
     }
     return YUF_OK;
 }
@@ -291,6 +327,7 @@ int gemm_group(hipStream_t st, const GemmParams *ps, int count) {
 struct Act {
     hipStream_t st = nullptr;
     float *h, *xn, *mix, *r, *k, *v, *wr, *al, *g, *lr, *y, *z, *rosa3, *rread, *ffn, *hl;
+    float *rz, *rcarry, *rends;  // segmented ROSA scratch (segment rows of kRosaSeg tokens)
     const int *tokens, *slots;
 };
 
@@ -306,6 +343,8 @@ Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
     a.rosa3 = e.rosa3 + m0 * 3 * s.rosa; a.rread = e.rread + m0 * s.rosa;
     a.ffn = e.ffn + m0 * 4 * d;
     a.hl = e.hl + (size_t)s0 * d;
+    const size_t seg0 = (m0 / kRosaSeg) * s.rosa;
+    a.rz = e.rz + seg0; a.rcarry = e.rcarry + seg0; a.rends = e.rends + seg0;
     a.tokens = e.tokens_dev + m0;
     a.slots = e.slots_dev + s0;
     return a;
@@ -394,7 +433,11 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         }
         rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
         rp.memory_in = ros; rp.memory_out = ros; rp.slot = a.slots; rp.read_out = a.rread;
-        ENG_TRY(launch_rosa(rp, st), "rosa");
+        if (e.rosa_segmented && Tc > 1 && rosa_segmented_ok(Tc, D, kRosaSeg)) {
+            ENG_TRY(launch_rosa_segmented(rp, w.rosa_al, kRosaSeg, a.rz, a.rcarry, a.rends, st), "rosa segmented");
+        } else {
+            ENG_TRY(launch_rosa(rp, st), "rosa");
+        }
         if ((rc = gemm(e, st, M, d, D, a.rread, D, w.rosa_out, D, a.h, d, nullptr, ACT_NONE, a.h, d)) != YUF_OK)
             return rc;
         // FFN
@@ -578,6 +621,7 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
     Engine &e = h->e;
     e.s = s;
     if (const char *ng = std::getenv("YUF_NO_GRAPH")) e.use_graphs = std::strcmp(ng, "1") != 0;
+    if (const char *rs = std::getenv("YUF_ROSA_SEGMENTED")) e.rosa_segmented = std::strcmp(rs, "0") != 0;
     e.max_streams = max_streams;
     e.max_tokens = max_tokens;
 
@@ -620,6 +664,7 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
         w.ln_o_w = nxt(); w.ln_o_b = nxt(); w.ln_r_w = nxt(); w.ln_r_b = nxt();
         w.rosa_w3 = nxt(); w.rosa_b3 = nxt(); w.rosa_hh = nxt(); w.rosa_decay = nxt(); w.rosa_out = nxt();
         w.ln_f_w = nxt(); w.ln_f_b = nxt(); w.ffn_cat = nxt(); w.ffn_out = nxt();
+        w.rosa_al = nxt();
     }
 
     // State: [layer][slot][...] for each of prev, wkv, rosa.
@@ -648,14 +693,15 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
     e.gemm_ws_floats = ws;
     const size_t sizes[] = {Mx * d, Mx * d, 6 * Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d,
                             3 * Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
-                            (size_t)max_streams * d, ws};
+                            (size_t)max_streams * d, ws, Mx / kRosaSeg * s.rosa + s.rosa, Mx / kRosaSeg * s.rosa + s.rosa,
+                            Mx / kRosaSeg * s.rosa + s.rosa};
     size_t total = 0;
     for (size_t z : sizes) total += ((z * sizeof(float) + 255) / 256) * 256;
     ENG_TRY(hipMalloc(&e.work.p, total), "workspace alloc");
     {
         char *cur = static_cast<char *>(e.work.p);
         float **dst[] = {&e.h, &e.xn, &e.mix, &e.r, &e.k, &e.v, &e.wr, &e.al, &e.g, &e.lr, &e.y, &e.z, &e.rosa3,
-                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws};
+                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.rends};
         for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
     }
     const size_t io_bytes = 256 * 3 + (size_t)(max_streams + max_tokens + 1) * sizeof(int);

@@ -50,6 +50,13 @@ struct RosaParams {
     const float *e_pre = nullptr, *g_pre = nullptr;
 };
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream);
+// Long sequences with the model's constant transition A = diag(lambda) H: the
+// T tokens of each chain split into T / L segments scanned in parallel (zero
+// start, then true start) around a carry pass with AL = A^L ([D][D] row-major,
+// fp32).  Scratch: z, carry, ends of B * (T / L) * D floats each.
+bool rosa_segmented_ok(int T, int D, int L);
+hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry, float *ends,
+                                 hipStream_t stream);
 
 // ----------------------------------------------------------------------- GEMM
 // C[m, n] = epilogue( sum_k A[m, k] * W[n, k] )   (nn.Linear: y = x W^T)

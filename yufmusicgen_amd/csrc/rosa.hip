@@ -146,6 +146,7 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
         }
     };
     auto emit = [&](int ch) {  // O(ch)
+        if (!p.read_out) return;  // end states only (first pass of the segmented scan)
         const int s = ch % kStages, t0 = ch * C, nt = min(C, p.T - t0);
         const size_t obase = (size_t)(bb * p.T + t0) * D;
         const auto ro = make_rsrc(p.read_out + obase, (uint32_t)(nt * D * 4));
@@ -397,6 +398,74 @@ __global__ void __launch_bounds__(256) rosa_step_kernel(RosaParams p) {
             if (p.memory_out) p.memory_out[(size_t)slot * D + c] = m[e];
         }
     }
+}
+
+// Segmented scan, carry pass.  With a constant transition A = diag(lambda) H,
+// the state after segment s of length L is m_{s+1} = A^L m_s + z_s, where z_s
+// is the segment's end state from a zero start.  One workgroup per chain walks
+// its P segments: it records each segment's start state (carry) and applies
+// A^L (row-major [D][D], each thread holding 64 entries of one row in
+// registers) plus z_s.  D in {64, 128, 256}: blockDim = D * D / 64.
+__global__ void __launch_bounds__(1024) rosa_carry_kernel(int P, int D, const float *AL, const float *z,
+                                                          const float *memory_in, const int *slot, float *carry) {
+    __shared__ float st[256];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    const int tpr = D / 64, r = tid / tpr, q = tid - r * tpr;
+    float arow[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) arow[j] = AL[(size_t)r * D + q * 64 + j];
+    const int sl = slot ? slot[b] : b;
+    if (tid < D) st[tid] = memory_in ? memory_in[(size_t)sl * D + tid] : 0.0f;
+    __syncthreads();
+    for (int s = 0; s < P; ++s) {
+        const size_t v = (size_t)b * P + s;
+        if (tid < D) carry[v * D + tid] = st[tid];
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 64; ++j) dot = fmaf(arow[j], st[q * 64 + j], dot);
+        // the tpr partial dot products of a row sit in adjacent lanes
+        for (int o = 1; o < tpr; o <<= 1) dot += __shfl_xor(dot, o);
+        __syncthreads();
+        if (q == 0) st[r] = dot + z[v * D + r];
+        __syncthreads();
+    }
+}
+
+__global__ void rosa_final_kernel(int P, int D, const float *ends, const int *slot, float *memory_out) {
+    const int b = blockIdx.x;
+    const int sl = slot ? slot[b] : b;
+    for (int c = threadIdx.x; c < D; c += blockDim.x)
+        memory_out[(size_t)sl * D + c] = ends[((size_t)b * P + P - 1) * D + c];
+}
+
+bool rosa_segmented_ok(int T, int D, int L) {
+    return L > 0 && T % L == 0 && T / L >= 2 && (D == 64 || D == 128 || D == 256);
+}
+
+hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry, float *ends,
+                                 hipStream_t stream) {
+    if (p.B <= 0) return hipSuccess;
+    if (!rosa_segmented_ok(p.T, p.D, L)) return hipErrorInvalidValue;
+    const int P = p.T / L;
+    // 1. every segment from a zero state: end states only.
+    RosaParams a = p;
+    a.B = p.B * P; a.T = L;
+    a.memory_in = nullptr; a.slot = nullptr; a.memory_out = z; a.read_out = nullptr;
+    hipError_t e = launch_rosa(a, stream);
+    if (e != hipSuccess) return e;
+    // 2. chain the segment start states.
+    hipLaunchKernelGGL(rosa_carry_kernel, dim3(p.B), dim3(p.D * p.D / 64), 0, stream, P, p.D, AL, z, p.memory_in,
+                       p.slot, carry);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    // 3. every segment again from its true start: the reads and end states.
+    RosaParams c = p;
+    c.B = p.B * P; c.T = L;
+    c.memory_in = carry; c.slot = nullptr; c.memory_out = ends;
+    if ((e = launch_rosa(c, stream)) != hipSuccess) return e;
+    // 4. the last segment's end state is the chain's new state.
+    if (p.memory_out)
+        hipLaunchKernelGGL(rosa_final_kernel, dim3(p.B), dim3(256), 0, stream, P, p.D, ends, p.slot, p.memory_out);
+    return hipGetLastError();
 }
 
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
