@@ -204,34 +204,37 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmGroup g, int per
 // for lane group g on both operands).
 // ---------------------------------------------------------------------------
 typedef float floatx4 __attribute__((ext_vector_type(4)));
-constexpr int kBigBM = 256, kBigBK = 16, kBigLd = kBigBK + 4, kBigThreads = 512;
+constexpr int kBigBM = 256, kBigThreads = 512;
+// K tile: 32 where the accumulators leave room for the larger load set, else 16.
+template <int BN> constexpr int big_bk() { return BN >= 256 ? 16 : 32; }
 
-template <int ROWS>
+template <int ROWS, int BK>
 struct BigLoad {
-    static constexpr int kF4 = ROWS * (kBigBK / 4);                    // float4 per tile
+    static constexpr int kF4 = ROWS * (BK / 4);                        // float4 per tile
     static constexpr int kPer = (kF4 + kBigThreads - 1) / kBigThreads;  // per thread
     float4 v[kPer];
 };
 
-template <int ROWS>
-__device__ __forceinline__ void big_load(BigLoad<ROWS> &t, __amdgpu_buffer_rsrc_t rsrc, int ld, int k0, int K,
+template <int ROWS, int BK>
+__device__ __forceinline__ void big_load(BigLoad<ROWS, BK> &t, __amdgpu_buffer_rsrc_t rsrc, int ld, int k0, int K,
                                          int tid) {
 #pragma unroll
-    for (int i = 0; i < BigLoad<ROWS>::kPer; ++i) {
+    for (int i = 0; i < BigLoad<ROWS, BK>::kPer; ++i) {
         const int q = tid + i * kBigThreads;
-        const int row = q >> 2, k = k0 + (q & 3) * 4;
+        const int row = q / (BK / 4), k = k0 + (q % (BK / 4)) * 4;
         // K % 4 == 0 on this path: a float4 is wholly inside or outside [0, K).
-        const uint32_t off = (q < BigLoad<ROWS>::kF4 && k < K) ? (uint32_t)((size_t)row * ld + k) * 4u : kBufferOob;
+        const uint32_t off = (q < BigLoad<ROWS, BK>::kF4 && k < K) ? (uint32_t)((size_t)row * ld + k) * 4u : kBufferOob;
         t.v[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
     }
 }
 
-template <int ROWS>
-__device__ __forceinline__ void big_store(const BigLoad<ROWS> &t, float *lds, int tid) {
+template <int ROWS, int BK>
+__device__ __forceinline__ void big_store(const BigLoad<ROWS, BK> &t, float *lds, int tid) {
+    constexpr int LD = BK + 4;
 #pragma unroll
-    for (int i = 0; i < BigLoad<ROWS>::kPer; ++i) {
+    for (int i = 0; i < BigLoad<ROWS, BK>::kPer; ++i) {
         const int q = tid + i * kBigThreads;
-        if (q < BigLoad<ROWS>::kF4) *reinterpret_cast<float4 *>(lds + (q >> 2) * kBigLd + (q & 3) * 4) = t.v[i];
+        if (q < BigLoad<ROWS, BK>::kF4) *reinterpret_cast<float4 *>(lds + (q / (BK / 4)) * LD + (q % (BK / 4)) * 4) = t.v[i];
     }
 }
 
@@ -247,6 +250,7 @@ __device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4
 template <int BN, bool STAGED>
 __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int per_xcd) {
     constexpr int WN = BN / 2, NT = WN / 16;
+    constexpr int kBigBK = big_bk<BN>(), kBigLd = kBigBK + 4;
     __shared__ __attribute__((aligned(16))) float lds[2 * (kBigBM + BN) * kBigLd];
     float(*As)[kBigBM * kBigLd] = reinterpret_cast<float(*)[kBigBM * kBigLd]>(lds);
     float(*Bs)[BN * kBigLd] = reinterpret_cast<float(*)[BN * kBigLd]>(lds + 2 * kBigBM * kBigLd);
@@ -272,8 +276,8 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
         for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int k_tiles = (p.K + kBigBK - 1) / kBigBK;
-    BigLoad<kBigBM> ta;
-    BigLoad<BN> tb;
+    BigLoad<kBigBM, kBigBK> ta;
+    BigLoad<BN, kBigBK> tb;
     big_load(ta, ra, p.lda, 0, p.K, tid);
     big_load(tb, rw, p.ldw, 0, p.K, tid);
     big_store(ta, As[0], tid);
@@ -287,20 +291,23 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
             big_load(ta, ra, p.lda, (kt + 1) * kBigBK, p.K, tid);
             big_load(tb, rw, p.ldw, (kt + 1) * kBigBK, p.K, tid);
         }
-        floatx4 af[4], bf[NT];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            af[i] = *reinterpret_cast<const floatx4 *>(As[cur] + (wm * 64 + i * 16 + li) * kBigLd + 4 * g4);
-#pragma unroll
-        for (int j = 0; j < NT; ++j)
-            bf[j] = *reinterpret_cast<const floatx4 *>(Bs[cur] + (wn * WN + j * 16 + li) * kBigLd + 4 * g4);
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int h = 0; h < kBigBK / 16; ++h) {  // 16 k per half: one ds_read_b128 per operand fragment
+            floatx4 af[4], bf[NT];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
+                af[i] = *reinterpret_cast<const floatx4 *>(As[cur] + (wm * 64 + i * 16 + li) * kBigLd + 16 * h + 4 * g4);
 #pragma unroll
-                for (int j = 0; j < NT; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][r], bf[j][r], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < NT; ++j)
+                bf[j] = *reinterpret_cast<const floatx4 *>(Bs[cur] + (wn * WN + j * 16 + li) * kBigLd + 16 * h + 4 * g4);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < NT; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][r], bf[j][r], acc[i][j], 0, 0, 0);
+        }
         if (more) {
             big_store(ta, As[cur ^ 1], tid);
             big_store(tb, Bs[cur ^ 1], tid);
