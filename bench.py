@@ -141,9 +141,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["scan", "prefill", "copy"], default=None,
-                    help="profiling aids: just the C2 scan (20 launches), just the prefill steps, or a plain "
-                         "256 MiB device copy (20 launches) that calibrates the FETCH_SIZE/WRITE_SIZE counters")
+    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy"], default=None,
+                    help="profiling aids: just the C2 scan (20 launches), just the prefill steps, just the C4 "
+                         "decode leg, or a plain 256 MiB device copy (20 launches) that calibrates the "
+                         "FETCH_SIZE/WRITE_SIZE counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -184,21 +185,23 @@ def main() -> int:
     def prefill_step():
         engine.prefill_device(tokens, logits, slots, logits="all")
 
-    log("prefill warmup")
-    for _ in range(args.warmup):
-        engine.reset_state()
-        prefill_step()
-    torch.cuda.synchronize()
-    log("prefill timed")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        prefill_step()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    ms_per_step = elapsed * 1e3 / args.steps
-    prefill_tps = B * T * args.steps / elapsed
-    log(f"prefill {ms_per_step:.2f} ms/step, {prefill_tps:.0f} tokens/s")
+    ms_per_step = prefill_tps = None
+    if args.only != "decode":
+        log("prefill warmup")
+        for _ in range(args.warmup):
+            engine.reset_state()
+            prefill_step()
+        torch.cuda.synchronize()
+        log("prefill timed")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            prefill_step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        ms_per_step = elapsed * 1e3 / args.steps
+        prefill_tps = B * T * args.steps / elapsed
+        log(f"prefill {ms_per_step:.2f} ms/step, {prefill_tps:.0f} tokens/s")
     if args.only == "prefill":
         print(json.dumps({"prefill_tokens_per_s": prefill_tps, "ms_per_step": ms_per_step}), flush=True)
         return 0
@@ -226,6 +229,10 @@ def main() -> int:
     dec_elapsed = time.perf_counter() - t0
     decode_tps = S * args.decode_steps / dec_elapsed
     log(f"decode {dec_elapsed * 1e3 / args.decode_steps:.3f} ms/step, {decode_tps:.0f} tokens/s")
+    if args.only == "decode":
+        print(json.dumps({"decode_tokens_per_s": decode_tps, "decode_ms_per_step": dec_elapsed * 1e3 / args.decode_steps}),
+              flush=True)
+        return 0
     engine.close()
     del logits
 
