@@ -23,8 +23,9 @@
 //                  accumulator tiles and runs the S-dependent products above,
 //                  16 NB + 16 v_mfma_f32_16x16x4f32 per chunk;
 //   one wave       stage B1: the four 16x16 Gram matrices (MFMA);
-//   NB waves       stage A: loads r, w, k, a, b, decays, running products and
-//                  the scaled operands -> LDS (16 columns each);
+//   NB waves       stage A: loads r, w, k, a, b (16-byte runs along the
+//                  columns, transposed through LDS), decays, running products
+//                  and the scaled operands -> LDS (16 columns each);
 //                  model path: kappa = normalize(k k_k), a = -kappa,
 //                  b = kappa alpha, k^ = k (1 + (alpha - 1) k_a) first;
 //   one wave       stage B2: (I - Gab)^{-1} by forward substitution, and in
@@ -83,7 +84,10 @@ struct Lds {
     static constexpr int kSlotT = 16 * kST;
     // Ring N (2): per-token 1 / max(|k k_k|, 1e-12) (model path).
     static constexpr int kSlotN = 16;
-    static constexpr int kFloats = 4 * kSlotA + 2 * kSlotH + 3 * kSlotG + 2 * kSlotT + 2 * kSlotN;
+    // Stage A transpose (one region per stage-A wave): up to 5 inputs x
+    // [16 tokens][16 columns], rows padded to kST floats.
+    static constexpr int kSlotR = 5 * 16 * kST;
+    static constexpr int kFloats = 4 * kSlotA + 2 * kSlotH + 3 * kSlotG + 2 * kSlotT + 2 * kSlotN + NB * kSlotR;
 };
 
 // Wave roles.  Waves w and w + 4 of a workgroup share a SIMD, and a wave
@@ -119,6 +123,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
     float *ringG = ringH + 2 * Ly::kSlotH;
     float *ringT = ringG + 3 * Ly::kSlotG;
     float *ringN = ringT + 2 * Ly::kSlotT;
+    float *stageR = ringN + 2 * Ly::kSlotN;
 
     // XCD-aware head index: consecutive heads of a batch row share an XCD's L2.
     const int flat = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
@@ -231,8 +236,11 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         // the 4 tokens; quarters are chained by a 2-step scan over lane groups.
         const int qg = lane >> 4;
         const int j = (role - kRoleA) * 16 + li;
-        const bool col_ok = j < N;
-        const uint32_t voff = col_ok ? (uint32_t)((4 * qg * HN + j) * 4) : kBufferOob;
+        // Loads: lane = (token li, 4-column group qg) reads 16 bytes per input,
+        // and the tile is transposed through LDS into the compute layout.
+        const int lc0 = (role - kRoleA) * 16 + 4 * qg;
+        const uint32_t voff = lc0 < N ? (uint32_t)((li * HN + lc0) * 4) : kBufferOob;
+        float *stR = stageR + (role - kRoleA) * Ly::kSlotR;
         constexpr int kIn = PREP ? 4 : 5;  // r, w, k, a(lpha) [, b]
         const float *src[5] = {p.r, p.w, p.k, p.a, PREP ? p.a : p.b};
         __amdgpu_buffer_rsrc_t rs[kIn];
@@ -240,18 +248,29 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         for (int x = 0; x < kIn; ++x) rs[x] = make_rsrc(src[x] + tok_base, tok_bytes);
         float kk_w = 0.0f, ka_w = 0.0f;
         if constexpr (PREP) {
+            const bool col_ok = j < N;
             kk_w = col_ok ? p.k_k[h * N + j] : 0.0f;
             ka_w = col_ok ? p.k_a[h * N + j] : 0.0f;
         }
+        floatx4 ld[kIn];
         float raw[kIn][4];
         auto load_chunk = [&](int c) {
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const int soff = c * chunk_bytes + tt * HN * 4;
+            for (int x = 0; x < kIn; ++x) ld[x] = buf_load4(rs[x], voff + c * chunk_bytes);
+        };
+        // ld (token li, columns 4 qg..) -> LDS -> raw (tokens 4 qg.., column li).
+        auto transpose = [&]() {
 #pragma unroll
-                for (int x = 0; x < kIn; ++x)
-                    raw[x][tt] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs[x], voff, soff, 0));
-            }
+            for (int x = 0; x < kIn; ++x)
+                *reinterpret_cast<floatx4 *>(stR + x * 16 * kST + li * kST + 4 * qg) = ld[x];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+            for (int x = 0; x < kIn; ++x)
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) raw[x][tt] = stR[x * 16 * kST + (4 * qg + tt) * kST + li];
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         };
         if (n_chunks > 0) load_chunk(0);
         const int rowbase = 4 * qg * SA + j;  // LDS [token][column] index of (4 qg, j)
@@ -259,6 +278,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
             const int c = it + 3;
             if (c >= 0 && c < n_chunks) {
                 wait_vmem();
+                transpose();
                 const int nt = min(kC, T - c * kC);
                 float *sA = ringA + (c & 3) * Ly::kSlotA;
                 float *sH = ringH + (c & 1) * Ly::kSlotH;
