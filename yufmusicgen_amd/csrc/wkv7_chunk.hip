@@ -22,10 +22,12 @@
 //   NB waves       consumers: wave q owns S^T[:, 16q..16q+15] as NB 16x16
 //                  accumulator tiles and runs the S-dependent products above,
 //                  16 NB + 16 v_mfma_f32_16x16x4f32 per chunk;
-//   one wave       stage B1: the four 16x16 Gram matrices (MFMA);
-//   NB waves       stage A: loads r, w, k, a, b (16-byte runs along the
-//                  columns, transposed through LDS), decays, running products
-//                  and the scaled operands -> LDS (16 columns each);
+//   one wave       stage B1: the four 16x16 Gram matrices (MFMA; B^ and K^
+//                  read from stage A's [key][token] tiles);
+//   NB waves       stage A: loads r, w, k, a, b, v (16-byte runs along the
+//                  columns; all but v transposed through LDS), decays, running
+//                  products (quarters joined by gfx950 row swaps) and the
+//                  scaled operands -> LDS (16 columns each);
 //                  model path: kappa = normalize(k k_k), a = -kappa,
 //                  b = kappa alpha, k^ = k (1 + (alpha - 1) k_a) first;
 //   one wave       stage B2: (I - Gab)^{-1} by forward substitution, and in
@@ -34,6 +36,12 @@
 // on i+1 and the consumers on chunk i, with one workgroup barrier per
 // iteration and ring buffers in LDS.  The consumers apply the chunk decay to
 // the state last:  S^T <- diag(g_15) (S0^T + B^^T U + K^^T V).
+// Global loads run two chunks ahead of their use in two register sets (loops
+// unrolled by two), so an HBM round trip (~1 us under load) spans two
+// iterations.  Only stage A and B2 load; the consumers read v from the ring
+// and only store, so no wave waits on a load issued after its own stores, and
+// the order of loads before each loop matches the loop's steady state (the
+// compiler's wait counts then allow the newer register set to stay in flight).
 //
 // MFMA operand layouts (16x16x4 f32; lane l, g = l / 16, li = l % 16):
 //   A operand A[m = li][k = g], B operand B[k = g][n = li],
@@ -73,11 +81,11 @@ template <int NB>
 struct Lds {
     static constexpr int NP = 16 * NB;        // padded head size
     static constexpr int SA = NP + 4;         // row stride of [token][column] tiles
-    // Ring A (4 chunks in flight): A~, R~ [16][SA]; B^^T, K^^T [NP][kST]; g_15 [NP].
+    // Ring A (4 chunks in flight): A~, R~ [16][SA]; B^^T, K^^T [NP][kST]; g_15 [NP];
+    // V^T [NP][kST] (value row, token).
     static constexpr int oAs = 0, oRs = 16 * SA, oBhT = 32 * SA, oKhT = oBhT + NP * kST, oGl = oKhT + NP * kST;
-    static constexpr int kSlotA = oGl + NP;
-    // Ring H (2): B^, K^ [16][SA] (Gram inputs only).
-    static constexpr int oBh = 0, oKh = 16 * SA, kSlotH = 32 * SA;
+    static constexpr int oV = oGl + NP;
+    static constexpr int kSlotA = oV + NP * kST;
     // Ring G (3): Gab^T [s][t], P, Qb, Qk [t][s], all [16][kST].
     static constexpr int oGabT = 0, oP = 16 * kST, oQb = 32 * kST, oQk = 48 * kST, kSlotG = 64 * kST;
     // Ring T (2): (I - Gab)^{-1} [16][kST].
@@ -87,7 +95,7 @@ struct Lds {
     // Stage A transpose (one region per stage-A wave): up to 5 inputs x
     // [16 tokens][16 columns], rows padded to kST floats.
     static constexpr int kSlotR = 5 * 16 * kST;
-    static constexpr int kFloats = 4 * kSlotA + 2 * kSlotH + 3 * kSlotG + 2 * kSlotT + 2 * kSlotN + NB * kSlotR;
+    static constexpr int kFloats = 4 * kSlotA + 3 * kSlotG + 2 * kSlotT + 2 * kSlotN + NB * kSlotR;
 };
 
 // Wave roles.  Waves w and w + 4 of a workgroup share a SIMD, and a wave
@@ -107,10 +115,6 @@ template <int NB> struct Roles {
     }
 };
 
-__device__ __forceinline__ float lane_from(float x, int src_lane) {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute((src_lane & 63) << 2, __float_as_int(x)));
-}
-
 template <int NB, bool PREP>
 __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
     wkv7_chunk_kernel(WkvParams p, int N, int heads, int per_xcd) {
@@ -119,8 +123,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
     constexpr int NP = Ly::NP, SA = Ly::SA;
     __shared__ __attribute__((aligned(16))) float lds[Ly::kFloats];
     float *ringA = lds;
-    float *ringH = ringA + 4 * Ly::kSlotA;
-    float *ringG = ringH + 2 * Ly::kSlotH;
+    float *ringG = ringA + 4 * Ly::kSlotA;
     float *ringT = ringG + 3 * Ly::kSlotG;
     float *ringN = ringT + 2 * Ly::kSlotT;
     float *stageR = ringN + 2 * Ly::kSlotN;
@@ -156,17 +159,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                 S[jb] = buf_load4(rs, (i < N && j0 < N) ? (uint32_t)(i * N + j0) * 4u : kBufferOob);
             }
         }
-        const auto rv = make_rsrc(p.v + tok_base, tok_bytes);
         const auto ry = make_rsrc(p.y + tok_base, tok_bytes);
-        float v[4];
-        auto load_v = [&](int c) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = c * kC + 4 * g + r;
-                v[r] = buf_load(rv, (t < T && i < N) ? (uint32_t)(t * HN + i) * 4u : kBufferOob);
-            }
-        };
-        if (n_chunks > 0) load_v(0);
         wait_vmem();
         for (int it = -4; it < n_chunks; ++it) {
             if (it >= 0) {
@@ -174,6 +167,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                 const float *sA = ringA + (c & 3) * Ly::kSlotA;
                 const float *sG = ringG + (c % 3) * Ly::kSlotG;
                 const float *sT = ringT + (c & 1) * Ly::kSlotT;
+                const floatx4 v = ld4(sA + Ly::oV + i * kST + 4 * g);  // V[4 g + r][i]
                 floatx4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
@@ -212,7 +206,6 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                     for (int r = 0; r < 4; ++r) acc = mfma(kh4[r], v[r], acc);
                     S[jb] = acc * gl4;
                 }
-                if (c + 1 < n_chunks) load_v(c + 1);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int t = c * kC + 4 * g + r;
@@ -241,8 +234,9 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         const int lc0 = (role - kRoleA) * 16 + 4 * qg;
         const uint32_t voff = lc0 < N ? (uint32_t)((li * HN + lc0) * 4) : kBufferOob;
         float *stR = stageR + (role - kRoleA) * Ly::kSlotR;
-        constexpr int kIn = PREP ? 4 : 5;  // r, w, k, a(lpha) [, b]
-        const float *src[5] = {p.r, p.w, p.k, p.a, PREP ? p.a : p.b};
+        constexpr int kT = PREP ? 4 : 5;  // transposed inputs r, w, k, a(lpha) [, b]
+        constexpr int kIn = kT + 1;       // + v (input kT), stored untransposed
+        const float *src[6] = {p.r, p.w, p.k, p.a, PREP ? p.v : p.b, p.v};
         __amdgpu_buffer_rsrc_t rs[kIn];
 #pragma unroll
         for (int x = 0; x < kIn; ++x) rs[x] = make_rsrc(src[x] + tok_base, tok_bytes);
@@ -252,36 +246,43 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
             kk_w = col_ok ? p.k_k[h * N + j] : 0.0f;
             ka_w = col_ok ? p.k_a[h * N + j] : 0.0f;
         }
-        floatx4 ld[kIn];
-        float raw[kIn][4];
-        auto load_chunk = [&](int c) {
+        // Inputs of even and odd chunks (two register sets).
+        floatx4 ld0[kIn], ld1[kIn];
+        float raw[kT][4];
+        auto load_chunk = [&](floatx4 (&ld)[kIn], int c) {
 #pragma unroll
             for (int x = 0; x < kIn; ++x) ld[x] = buf_load4(rs[x], voff + c * chunk_bytes);
         };
         // ld (token li, columns 4 qg..) -> LDS -> raw (tokens 4 qg.., column li).
-        auto transpose = [&]() {
+        auto transpose = [&](const floatx4 (&ld)[kIn]) {
 #pragma unroll
-            for (int x = 0; x < kIn; ++x)
+            for (int x = 0; x < kT; ++x)
                 *reinterpret_cast<floatx4 *>(stR + x * 16 * kST + li * kST + 4 * qg) = ld[x];
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-            for (int x = 0; x < kIn; ++x)
+            for (int x = 0; x < kT; ++x)
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) raw[x][tt] = stR[x * 16 * kST + (4 * qg + tt) * kST + li];
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         };
-        if (n_chunks > 0) load_chunk(0);
+        // Unconditional (a chunk past T reads zeros) and not interleaved (the
+        // scheduling barrier): the compiler's wait counts at the loop head
+        // follow the order of these loads.
+        load_chunk(ld0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_chunk(ld1, 1);
         const int rowbase = 4 * qg * SA + j;  // LDS [token][column] index of (4 qg, j)
-        for (int it = -4; it < n_chunks; ++it) {
-            const int c = it + 3;
-            if (c >= 0 && c < n_chunks) {
-                wait_vmem();
-                transpose();
-                const int nt = min(kC, T - c * kC);
+        // Chunk c (iteration c - 3); its set is reloaded with chunk c + 2.
+        auto body = [&](int c, floatx4 (&ld)[kIn], bool load_next) {
+            {
                 float *sA = ringA + (c & 3) * Ly::kSlotA;
-                float *sH = ringH + (c & 1) * Ly::kSlotH;
+                transpose(ld);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) sA[Ly::oV + (lc0 + e) * kST + li] = ld[kT][e];
+                if (load_next) load_chunk(ld, c + 2);
+                const int nt = min(kC, T - c * kC);
                 float av[4], bv[4], kv[4], rv[4], dv[4];
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) {
@@ -318,20 +319,19 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                         gl[tt] = gacc;
                     }
                 }
-                // Inclusive scan of the quarter end products over the four lane
-                // groups, then shift by one group: base = product of d over the
-                // earlier quarters.  (Cross-lane reads run on every lane, outside
-                // any condition.)
-                float s1 = gl[3];
-                const float x1 = lane_from(s1, lane - 16);
-                s1 = qg >= 1 ? s1 * x1 : s1;
-                const float x2 = lane_from(s1, lane - 32);
-                s1 = qg >= 2 ? s1 * x2 : s1;
-                const float prev = lane_from(s1, lane - 16);
-                const float base = qg >= 1 ? prev : 1.0f;
+                // base = product of d over the earlier quarters (exclusive scan of
+                // the quarter end products e_q over the four 16-lane rows), with
+                // the gfx950 row swaps: P = {e0, e0, e2, e2}, Q = {e1, e1, e3, e3},
+                // R = e0 e1 on every row.  (Run on every lane, outside any condition.)
+                const float eq = gl[3];
+                const auto sw16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(eq), __float_as_uint(eq), false, false);
+                const float P = __uint_as_float(sw16[0]), Q = __uint_as_float(sw16[1]);
+                const float m01 = P * Q;
+                const auto sw32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m01), __float_as_uint(m01), false, false);
+                const float R = __uint_as_float(sw32[0]);
+                const float base = qg == 0 ? 1.0f : qg == 1 ? P : qg == 2 ? R : R * P;
                 float bh[4], kh[4];
                 float *pAs = sA + Ly::oAs + rowbase, *pRs = sA + Ly::oRs + rowbase;
-                float *pBh = sH + Ly::oBh + rowbase, *pKh = sH + Ly::oKh + rowbase;
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) {
                     const float gprev = tt == 0 ? base : base * gl[tt - 1];
@@ -341,31 +341,47 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                     kh[tt] = kv[tt] * ig;
                     pAs[tt * SA] = av[tt] * gprev;
                     pRs[tt * SA] = rv[tt] * gam;
-                    pBh[tt * SA] = bh[tt];
-                    pKh[tt * SA] = kh[tt];
                 }
                 *reinterpret_cast<floatx4 *>(sA + Ly::oBhT + j * kST + 4 * qg) = floatx4{bh[0], bh[1], bh[2], bh[3]};
                 *reinterpret_cast<floatx4 *>(sA + Ly::oKhT + j * kST + 4 * qg) = floatx4{kh[0], kh[1], kh[2], kh[3]};
                 if (qg == 3) sA[Ly::oGl + j] = base * gl[3];
-                // Next chunk's loads go out after the last use of this one's registers.
-                if (c + 1 < n_chunks) load_chunk(c + 1);
             }
             lds_barrier();
+        };
+        // Iteration -4 has no stage-A chunk.  The steady loop loads
+        // unconditionally (the same issue order as before the loop: the even
+        // set, then the odd one); the last chunks and the three iterations
+        // after stage A's last chunk follow it.
+        lds_barrier();
+        int c = 0;
+        for (; c + 3 < n_chunks; c += 2) {
+            body(c, ld0, true);
+            body(c + 1, ld1, true);
         }
+        if (c < n_chunks) body(c, ld0, c + 2 < n_chunks);
+        if (c + 1 < n_chunks) body(c + 1, ld1, false);
+        if (c + 2 < n_chunks) body(c + 2, ld0, false);
+        for (int k = 0; k < 3; ++k) lds_barrier();
     } else if (role == kRoleB1) {
         // ------------------------------------------------------------ stage B1
         for (int it = -4; it < n_chunks; ++it) {
             const int c = it + 2;
             if (c >= 0 && c < n_chunks) {
                 const float *sA = ringA + (c & 3) * Ly::kSlotA;
-                const float *sH = ringH + (c & 1) * Ly::kSlotH;
                 float *sG = ringG + (c % 3) * Ly::kSlotG;
                 floatx4 gab = {0.f, 0.f, 0.f, 0.f}, gp = gab, gqb = gab, gqk = gab;
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
                     const int o = li * SA + 16 * jb + 4 * g;
                     const floatx4 a4 = ld4(sA + Ly::oAs + o), r4 = ld4(sA + Ly::oRs + o);
-                    const floatx4 b4 = ld4(sH + Ly::oBh + o), k4 = ld4(sH + Ly::oKh + o);
+                    // B^[s = li][key 16 jb + 4 g + r] from the [key][token] tiles.
+                    const int oT = (16 * jb + 4 * g) * kST + li;
+                    floatx4 b4, k4;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        b4[r] = sA[Ly::oBhT + oT + r * kST];
+                        k4[r] = sA[Ly::oKhT + oT + r * kST];
+                    }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         gab = mfma(a4[r], b4[r], gab);
@@ -390,11 +406,11 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         }
     } else {
         // ------------------------------------------------------------ stage B2
-        // (model path) per-token inverse key norms one chunk ahead of stage A:
+        // (model path) per-token inverse key norms one iteration ahead of stage A:
         // lane = (token li, column group g + 4 m), partial sums folded over the
         // four lane groups.
         __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + tok_base, tok_bytes);
-        floatx4 kkw[NB], kraw[NB];
+        floatx4 kkw[NB], kraw0[NB], kraw1[NB];  // k of even / odd chunks
         if constexpr (PREP) {
 #pragma unroll
             for (int m = 0; m < NB; ++m) {
@@ -403,7 +419,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                 for (int e = 0; e < 4; ++e) kkw[m][e] = j0 < N ? p.k_k[h * N + j0 + e] : 0.0f;
             }
         }
-        auto load_k = [&](int c) {
+        auto load_k = [&](floatx4 (&kraw)[NB], int c) {
 #pragma unroll
             for (int m = 0; m < NB; ++m) {
                 const int j0 = 4 * (g + 4 * m);
@@ -411,12 +427,15 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                 kraw[m] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, c * chunk_bytes, 0));
             }
         };
-        if (PREP && n_chunks > 0) load_k(0);
-        for (int it = -4; it < n_chunks; ++it) {
+        if constexpr (PREP) {  // unconditional and in order, as in stage A
+            load_k(kraw0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            load_k(kraw1, 1);
+        }
+        auto step = [&](int it, floatx4 (&kraw)[NB], bool load_next) {
             if constexpr (PREP) {
                 const int cn = it + 4;
                 if (cn < n_chunks) {
-                    wait_vmem();
                     float sq = 0.0f;
 #pragma unroll
                     for (int m = 0; m < NB; ++m)
@@ -425,9 +444,12 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                             const float x = kraw[m][e] * kkw[m][e];
                             sq = fmaf(x, x, sq);
                         }
-                    if (cn + 1 < n_chunks) load_k(cn + 1);
-                    sq += lane_from(sq, lane ^ 16);
-                    sq += lane_from(sq, lane ^ 32);
+                    if (load_next) load_k(kraw, cn + 2);
+                    // Sum over the four 16-lane rows with the gfx950 row swaps.
+                    const auto p16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(sq), __float_as_uint(sq), false, false);
+                    sq = __uint_as_float(p16[0]) + __uint_as_float(p16[1]);
+                    const auto p32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(sq), __float_as_uint(sq), false, false);
+                    sq = __uint_as_float(p32[0]) + __uint_as_float(p32[1]);
                     if (lane < kC) ringN[(cn & 1) * Ly::kSlotN + lane] = 1.0f / fmaxf(sqrtf(sq), 1e-12f);
                 }
             }
@@ -457,6 +479,17 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
                 }
             }
             lds_barrier();
+        };
+        // Chunk cn = it + 4 is even for even it, so kraw0 (loaded first) is used
+        // first; the steady loop loads unconditionally, the tail as needed.
+        int it = -4;
+        for (; it + 7 < n_chunks; it += 2) {
+            step(it, kraw0, true);
+            step(it + 1, kraw1, true);
+        }
+        for (; it < n_chunks; it += 2) {
+            step(it, kraw0, it + 6 < n_chunks);
+            if (it + 1 < n_chunks) step(it + 1, kraw1, it + 7 < n_chunks);
         }
     }
 }
