@@ -120,6 +120,22 @@ int yuf_ln_linear_f32(int M, int N, int K, const float *A, const float *gamma, c
                       const float *gate, const float *W, const float *bias, const float *residual, float *C,
                       void *stream);
 
+/*
+ * bf16-weight forms of yuf_linear_f32 / yuf_ln_linear_f32 (the C5
+ * configuration's weight type; no counterpart in the fp32 reference kernels,
+ * they replace the same nn.Linear call sites).  W is [N, K] bf16 (raw 16-bit
+ * patterns, uint16_t); A, bias, residual and C are fp32.  A is rounded to bf16
+ * (nearest even) as it enters the matrix cores; accumulation is fp32.
+ * Needs K % 8 == 0; for M > 64, N % 64 == 0 or N % 160 == 0.
+ */
+int yuf_linear_bf16w(int M, int N, int K, const float *A, const uint16_t *W,
+                     const float *bias, int act, const float *residual, float *C,
+                     void *stream);
+int yuf_ln_linear_bf16w(int M, int N, int K, const float *A, const float *gamma,
+                        const float *beta, const float *gate, const uint16_t *W,
+                        const float *bias, const float *residual, float *C,
+                        void *stream);
+
 /* ---------------------------------------------------------------------------
  * Checkpoints (.yuf).  Replaces `Checkpoint::load / tensor / tensor_dims`
  * (vulkan/src/checkpoint.rs:90-176).
@@ -166,6 +182,21 @@ enum { YUF_LOGITS_NONE = 0, YUF_LOGITS_LAST = 1, YUF_LOGITS_ALL = 2 };
  * max_tokens = largest n * T processed per internal pass (longer prefills
  * are split into T-chunks that carry the state). */
 int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_tokens, yuf_engine **out);
+
+/* Projection-weight type for yuf_engine_create_ex. */
+enum { YUF_WEIGHTS_F32 = 0, YUF_WEIGHTS_BF16 = 1 };
+
+/* yuf_engine_create with a projection-weight type (the `weight_dtype`
+ * argument of the engine API; the C5 configuration runs bf16 weights with
+ * fp32 accumulation, yufmusicgen/config.py:73-93).  YUF_WEIGHTS_BF16 keeps a
+ * bf16 copy (round to nearest even, or the file's own bf16 values) of every
+ * nn.Linear weight and the tied LM head; the GEMMs round their fp32
+ * activations to bf16 and accumulate in fp32.  Everything else (LayerNorm,
+ * the WKV-7 and ROSA recurrences, state) stays fp32.  Needs d_model, the
+ * low-rank width and rosa_size to be multiples of 8, and the prefill GEMM
+ * widths (d, low rank, 3 rosa_size, vocab) multiples of 64 or 160. */
+int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int max_tokens, int weight_type,
+                         yuf_engine **out);
 void yuf_engine_destroy(yuf_engine *eng);
 int yuf_engine_config(const yuf_engine *eng, yuf_model_config *out);
 /* The HIP stream the engine runs its work on (hipStream_t as void*). */

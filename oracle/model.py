@@ -13,6 +13,13 @@ Follows ``yufmusicgen/model.py`` op for op with ``use_cuda_kernel=False`` and
 
 Weights are a dict keyed by the reference's ``state_dict`` names (the names
 the ``.yuf`` container carries, ``vulkan/src/compute/model.rs:916-951``).
+
+``bf16_linear=True`` restates the bf16-weight configuration (C5's weight type,
+fp32 accumulation): every nn.Linear weight and the LM head (not the embedding
+gather) is rounded to bf16, and every projection input is rounded to bf16
+before its product; products accumulate in ``dtype``; everything else (norms,
+gates, both recurrences) is unchanged.  Rounding is torch's float32 ->
+bfloat16 cast (round to nearest even).
 """
 
 from __future__ import annotations
@@ -36,10 +43,23 @@ class LayerState:
     rosa: torch.Tensor  # [B, D]
 
 
+# nn.Linear weights (by name suffix), including the low-rank pairs.
+_LINEAR_SUFFIXES = (
+    "receptance.weight", "key.weight", "value.weight", "output.weight", "time_mix.w1", "time_mix.w2",
+    "time_mix.a1", "time_mix.a2", "time_mix.g1", "time_mix.g2", "input.weight", "write_gate.weight",
+    "read_gate.weight", "ffn_in.weight", "ffn_gate.weight", "ffn_out.weight",
+)
+
+
+def _bf16(x: torch.Tensor) -> torch.Tensor:
+    return x.to(torch.float32).to(torch.bfloat16).to(x.dtype)
+
+
 class OracleModel:
-    def __init__(self, config: dict, weights: dict, dtype=torch.float64):
+    def __init__(self, config: dict, weights: dict, dtype=torch.float64, bf16_linear: bool = False):
         self.cfg = dict(config)
         self.dtype = dtype
+        self.bf16_linear = bool(bf16_linear)
         self.d = int(self.cfg["d_model"])
         self.n_layers = int(self.cfg["n_layers"])
         self.heads = int(self.cfg["n_heads"])
@@ -50,6 +70,10 @@ class OracleModel:
         if "lm_head.weight" not in self.w:
             # Tied head (model.py:390-391; export_checkpoint.py:70-74).
             self.w["lm_head.weight"] = self.w["token_embedding.weight"]
+        if self.bf16_linear:
+            for name in list(self.w):
+                if name == "lm_head.weight" or name.endswith(_LINEAR_SUFFIXES):
+                    self.w[name] = _bf16(self.w[name])
 
     # ------------------------------------------------------------------ state
     def initial_state(self, batch: int) -> list:
@@ -69,6 +93,10 @@ class OracleModel:
     def _ln(self, x, layer_prefix: str):
         return F.layer_norm(x, (self.d,), self.w[layer_prefix + ".weight"], self.w[layer_prefix + ".bias"], LN_EPS)
 
+    def _mm(self, x: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
+        """x @ m for a projection (m already in its product orientation)."""
+        return (_bf16(x) if self.bf16_linear else x) @ m
+
     # ---------------------------------------------------------------- TimeMix
     def timemix_inputs(self, layer: int, x: torch.Tensor, previous: torch.Tensor):
         """model.py:97-131: returns (r, w_raw, k_adjusted, v, -kk, kk*a, g)."""
@@ -81,12 +109,13 @@ class OracleModel:
         xv = x + delta * p("mix_v")
         xa = x + delta * p("mix_a")
         xg = x + delta * p("mix_g")
-        r = xr @ p("receptance.weight").T
-        w = p("w0") + torch.tanh(xw @ p("w1")) @ p("w2")
-        k = xk @ p("key.weight").T
-        v = xv @ p("value.weight").T
-        a = torch.sigmoid(p("a0") + (xa @ p("a1")) @ p("a2"))
-        g = torch.sigmoid((xg @ p("g1")) @ p("g2"))
+        mm = self._mm
+        r = mm(xr, p("receptance.weight").T)
+        w = p("w0") + mm(torch.tanh(mm(xw, p("w1"))), p("w2"))
+        k = mm(xk, p("key.weight").T)
+        v = mm(xv, p("value.weight").T)
+        a = torch.sigmoid(p("a0") + mm(mm(xa, p("a1")), p("a2")))
+        g = torch.sigmoid(mm(mm(xg, p("g1")), p("g2")))
         batch, steps, _ = k.shape
         shape = (batch, steps, self.heads, self.head_size)
         kk = F.normalize((k * p("k_k")).view(shape), dim=-1, p=2.0, eps=1e-12)
@@ -100,19 +129,19 @@ class OracleModel:
         y = y.reshape(x.shape)
         p = lambda s: self._p(layer, "time_mix." + s)  # noqa: E731
         z = F.layer_norm(y, (self.d,), p("out_norm.weight"), p("out_norm.bias"), LN_EPS)
-        out = (z * g) @ p("output.weight").T
+        out = self._mm(z * g, p("output.weight").T)
         return out, x[:, -1].clone(), memory
 
     # ------------------------------------------------------------------- ROSA
     def rosa(self, layer: int, x: torch.Tensor, memory: torch.Tensor):
         p = lambda s: self._p(layer, "rosa." + s)  # noqa: E731
-        cand = x @ p("input.weight").T + p("input.bias")
-        write = x @ p("write_gate.weight").T + p("write_gate.bias")
-        read_gate = x @ p("read_gate.weight").T + p("read_gate.bias")
+        cand = self._mm(x, p("input.weight").T) + p("input.bias")
+        write = self._mm(x, p("write_gate.weight").T) + p("write_gate.bias")
+        read_gate = self._mm(x, p("read_gate.weight").T) + p("read_gate.bias")
         decay = torch.sigmoid(p("decay"))
         direction = F.normalize(p("householder"), dim=0)
         read, memory = rosa_scan(cand, write, read_gate, decay, direction, memory, gated=True)
-        return read @ p("output.weight").T, memory
+        return self._mm(read, p("output.weight").T), memory
 
     # ------------------------------------------------------------------ block
     def block(self, layer: int, x: torch.Tensor, state: LayerState):
@@ -122,8 +151,8 @@ class OracleModel:
         rosa_out, rosa_mem = self.rosa(layer, self._ln(x, pre + "norm_rosa"), state.rosa)
         x = x + rosa_out
         f = self._ln(x, pre + "norm_ffn")
-        hidden = F.silu(f @ self._p(layer, "ffn_in.weight").T) * (f @ self._p(layer, "ffn_gate.weight").T)
-        x = x + hidden @ self._p(layer, "ffn_out.weight").T
+        hidden = F.silu(self._mm(f, self._p(layer, "ffn_in.weight").T)) * self._mm(f, self._p(layer, "ffn_gate.weight").T)
+        x = x + self._mm(hidden, self._p(layer, "ffn_out.weight").T)
         return x, LayerState(previous, memory, rosa_mem)
 
     # ------------------------------------------------------------------ model
@@ -144,7 +173,7 @@ class OracleModel:
         if logits == "last":
             hidden = hidden[:, -1:]
         normed = F.layer_norm(hidden, (self.d,), self.w["final_norm.weight"], self.w["final_norm.bias"], LN_EPS)
-        out = normed @ self.w["lm_head.weight"].T
+        out = self._mm(normed, self.w["lm_head.weight"].T)
         return (out[:, -1] if logits == "last" else out), new_state
 
     def step(self, ids, state=None):

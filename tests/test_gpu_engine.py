@@ -191,6 +191,50 @@ def test_wide_model_prefill_and_decode_vs_oracle(tmp_path):
     assert got_dev <= 3.0 * fp32_dev + 1e-5, (got_dev, fp32_dev)
 
 
+def test_bf16_weights_engine_vs_bf16_oracle(tmp_path):
+    """bf16 projection weights (yuf_engine_create_ex) on the C5 architecture cut
+    to 2 layers (d = 1024, 16 x 64 heads, ROSA 256, V = 20480): 2 x 128 tokens
+    of prefill (the bf16 large-tile kernel) and two decode steps (the bf16 decode
+    kernel with LayerNorm prologues and the SiLU pair).  The oracle restates the
+    bf16 configuration (bf16 weights and projection inputs).  Two valid bf16
+    programs drift apart faster than fp32 ones (an activation near a bf16
+    rounding midpoint rounds either way, a 2^-8 step), so the bound is the
+    oracle's own float32 bf16 program's deviation from its float64 one (times
+    three, as for the fp32 wide model); and the engine must sit well inside the
+    distance between the bf16 and the fp32 configurations."""
+    import dataclasses
+    cfg = dataclasses.replace(PRESETS["wide"], n_layers=2)
+    weights = synth_weights(cfg, seed=8)
+    path = tmp_path / "w.yuf"
+    write_yuf(path, cfg, weights)
+    tokens = prompt_tokens(5, 2, 128, cfg.vocab_size)
+    nxt = uniform_tokens(6, 2, 2, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=2, max_tokens=256, weight_dtype="bf16")
+    got = [eng.prefill(tokens, logits="all")] + [eng.step(nxt[:, t]) for t in range(2)]
+    got_blob = _states_from_blob(eng, [0, 1])
+
+    def run(model):
+        out, st = model.forward(tokens)
+        outs = [out.numpy().astype(np.float64)]
+        for t in range(2):
+            out, st = model.step(nxt[:, t], st)
+            outs.append(out.numpy().astype(np.float64))
+        return outs, state_to_blob(st).astype(np.float64)
+
+    e64, e64_blob = run(OracleModel(cfg.to_dict(), weights, bf16_linear=True))
+    e32, e32_blob = run(OracleModel(cfg.to_dict(), weights, dtype=torch.float32, bf16_linear=True))
+    f64, f64_blob = run(OracleModel(cfg.to_dict(), weights))
+    pairs = [(f"logits {i}", g, a, b, c) for i, (g, a, b, c) in enumerate(zip(got, e64, e32, f64))]
+    pairs.append(("states", got_blob, e64_blob, e32_blob, f64_blob))
+    for name, g, ref, ref32, fp in pairs:
+        dev = float(np.abs(g - ref).max())
+        prog = float(np.abs(ref32 - ref).max())
+        effect = float(np.abs(fp - ref).max())
+        print(f"{name}: engine {dev:.3e}, float32 bf16 program {prog:.3e}, bf16 vs fp32 {effect:.3e}", flush=True)
+        assert dev <= 3.0 * prog + 1e-5, (name, dev, prog)
+        assert dev <= 0.5 * effect, (name, dev, effect)
+
+
 def test_rosa_segmented_prefill_matches_sequential(tmp_path, monkeypatch):
     """The segmented ROSA prefill (parallel 64-token segments around an A^64
     carry pass) against the sequential chunked scan, through the whole model:

@@ -74,3 +74,59 @@ def test_tiny_model_prompt_and_greedy_match_reference(golden_dir):
         token = torch.tensor([int(expect)])
         last, state = model.step(token, state)
         np.testing.assert_allclose(last.numpy()[0], z["greedy_logits"][i], rtol=1e-4, atol=1e-5)
+
+
+def _bf16_rne_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bfloat16 from the bit patterns (the
+    IEEE rule, written independently of torch), returned as float32."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def test_bf16_rounding_of_the_bf16_oracle():
+    """The bf16 configuration's rounding (torch's float32 -> bfloat16 cast) is
+    round-to-nearest-even: checked against the bit-level rule on random values,
+    exact ties (both directions) and values just off a tie."""
+    from oracle.model import _bf16
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0,
+                        # ties: low 16 bits exactly 0x8000, even and odd upper halves
+                        np.array([0x3F808000, 0x3F818000, 0xBF808000, 0xBF818000], dtype=np.uint32).view(np.float32),
+                        # one ulp either side of a tie
+                        np.array([0x3F808001, 0x3F807FFF], dtype=np.uint32).view(np.float32)])
+    got = _bf16(torch.from_numpy(x.astype(np.float64))).numpy().astype(np.float32)
+    np.testing.assert_array_equal(got, _bf16_rne_bits(x))
+    ties = np.array([0x3F808000, 0x3F818000], dtype=np.uint32).view(np.float32)
+    np.testing.assert_array_equal(_bf16(torch.from_numpy(ties.astype(np.float64))).numpy().astype(np.float32).view(np.uint32),
+                                  np.array([0x3F800000, 0x3F820000], dtype=np.uint32))
+
+
+def test_bf16_oracle_rounds_projection_operands_only():
+    """bf16_linear rounds the nn.Linear weights and the LM head, never the
+    embedding gather, the norms, the recurrence parameters or the biases; with
+    weights and a batch made of bf16 values the first projection's inputs
+    change only through the rounding of activations."""
+    cfg = PRESETS["tiny"]
+    weights = synth_weights(cfg, seed=3)
+    model = OracleModel(cfg.to_dict(), weights, bf16_linear=True)
+    plain = OracleModel(cfg.to_dict(), weights)
+    for name, value in model.w.items():
+        same = torch.equal(value, plain.w[name])
+        rounded = name == "lm_head.weight" or any(name.endswith(s) for s in
+                                                  ("receptance.weight", "key.weight", "value.weight",
+                                                   "output.weight", "w1", "w2", "a1", "a2", "g1", "g2",
+                                                   "input.weight", "write_gate.weight", "read_gate.weight",
+                                                   "ffn_in.weight", "ffn_gate.weight", "ffn_out.weight"))
+        if rounded:
+            np.testing.assert_array_equal(value.numpy().astype(np.float32),
+                                          _bf16_rne_bits(plain.w[name].numpy().astype(np.float32)))
+        else:
+            assert same, name
+    # The two configurations differ, by a bf16-sized amount.
+    ids = np.array([[1, 5, 9, 200]])
+    a, _ = model.forward(ids)
+    b, _ = plain.forward(ids)
+    rel = float((a - b).abs().max() / b.abs().max())
+    assert 1e-4 < rel < 5e-2, rel

@@ -47,6 +47,8 @@ SIGNATURES = {
     "yuf_rosa_scan_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_ln_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
+    "yuf_linear_bf16w": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
+    "yuf_ln_linear_bf16w": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_ckpt_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),
     "yuf_ckpt_free": (None, [c_void_p]),
     "yuf_ckpt_config": (ctypes.c_int, [c_void_p, ctypes.POINTER(ModelConfigC)]),
@@ -54,6 +56,7 @@ SIGNATURES = {
                                        ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
                                        ctypes.POINTER(ctypes.c_int64)]),
     "yuf_engine_create": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(c_void_p)]),
+    "yuf_engine_create_ex": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(c_void_p)]),
     "yuf_engine_destroy": (None, [c_void_p]),
     "yuf_engine_config": (ctypes.c_int, [c_void_p, ctypes.POINTER(ModelConfigC)]),
     "yuf_engine_stream": (c_void_p, [c_void_p]),

@@ -61,7 +61,12 @@ struct Engine {
     ModelShape s;
     int max_streams = 0, max_tokens = 0;
     hipStream_t stream = nullptr;
-    DeviceBuf weights, state, work, io;
+    DeviceBuf weights, weights_h, state, work, io;
+    // bf16 mode: a bf16 image of the weight buffer (same element offsets); the
+    // GEMMs of weights inside [w_base, w_base + w_floats) read it instead.
+    const float *w_base = nullptr;
+    size_t w_floats = 0;
+    const uint16_t *w_h = nullptr;
     std::vector<LayerW> layers;
     const float *emb = nullptr, *ln_fin_w = nullptr, *ln_fin_b = nullptr, *head = nullptr;
     // state arrays, [layer][slot][...]
@@ -284,6 +289,7 @@ GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, co
     p.M = M; p.N = N; p.K = K; p.A = A; p.lda = lda; p.W = W; p.ldw = ldw; p.C = C; p.ldc = ldc;
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = ldr; p.silu_pair = silu_pair;
     p.workspace = e.gemm_ws; p.workspace_floats = e.gemm_ws_floats;
+    if (e.w_h && W >= e.w_base && W < e.w_base + e.w_floats) p.Wh = e.w_h + (W - e.w_base);
     return p;
 }
 
@@ -605,10 +611,27 @@ struct yuf_engine {
 
 using yuf::fail;
 
+namespace {
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN), as v_cvt_pk_bf16_f32.
+uint16_t bf16_bits(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+}  // namespace
+
 extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_tokens, yuf_engine **out) {
+    return yuf_engine_create_ex(ckpt, max_streams, max_tokens, YUF_WEIGHTS_F32, out);
+}
+
+extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int max_tokens, int weight_type,
+                                    yuf_engine **out) {
     using namespace yuf;
     if (!ckpt || !out) return fail(YUF_ERR_INVALID, "yuf_engine_create: null argument");
     *out = nullptr;
+    if (weight_type != YUF_WEIGHTS_F32 && weight_type != YUF_WEIGHTS_BF16)
+        return fail(YUF_ERR_INVALID, "weight_type must be YUF_WEIGHTS_F32 or YUF_WEIGHTS_BF16");
     if (max_streams < 1 || max_tokens < 1) return fail(YUF_ERR_INVALID, "max_streams and max_tokens must be >= 1");
     const Checkpoint &ck = checkpoint_of(ckpt);
     const ModelShape &s = ck.shape;
@@ -616,6 +639,14 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
         return fail(YUF_ERR_INVALID, "head_size " + std::to_string(s.head_size) + " has no scan kernel");
     if (s.d > 64 * 32) return fail(YUF_ERR_INVALID, "d_model above 2048 is not supported");
     if (s.rosa > 1024) return fail(YUF_ERR_INVALID, "rosa_size above 1024 is not supported");
+    if (weight_type == YUF_WEIGHTS_BF16) {
+        auto wide_ok = [](long long n) { return n % 64 == 0 || n % 160 == 0; };
+        if (s.d % 8 != 0 || s.low_rank % 8 != 0 || s.rosa % 8 != 0)
+            return fail(YUF_ERR_INVALID, "bf16 weights need d_model, the low-rank width and rosa_size % 8 == 0");
+        if (!wide_ok(s.d) || !wide_ok(s.low_rank) || !wide_ok(3LL * s.rosa) || !wide_ok(s.vocab))
+            return fail(YUF_ERR_INVALID, "bf16 weights need d_model, the low-rank width, 3 rosa_size and the vocabulary "
+                                         "to be multiples of 64 or 160");
+    }
     std::unique_ptr<yuf_engine> h(new (std::nothrow) yuf_engine());
     if (!h) return fail(YUF_ERR_OOM, "host allocation failed");
     Engine &e = h->e;
@@ -648,6 +679,21 @@ extern "C" int yuf_engine_create(const yuf_ckpt *ckpt, int max_streams, int max_
     ENG_TRY(hipMalloc(&e.weights.p, host.size() * sizeof(float)), "weights alloc");
     ENG_TRY(hipMemcpy(e.weights.p, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice), "weights upload");
     const float *base = static_cast<const float *>(e.weights.p);
+    if (weight_type == YUF_WEIGHTS_BF16) {
+        std::vector<uint16_t> hb;
+        try {
+            hb.resize(host.size());
+        } catch (const std::bad_alloc &) {
+            return fail(YUF_ERR_OOM, "out of host memory preparing bf16 weights");
+        }
+        for (size_t i = 0; i < host.size(); ++i) hb[i] = bf16_bits(host[i]);
+        ENG_TRY(hipMalloc(&e.weights_h.p, hb.size() * sizeof(uint16_t)), "bf16 weights alloc");
+        ENG_TRY(hipMemcpy(e.weights_h.p, hb.data(), hb.size() * sizeof(uint16_t), hipMemcpyHostToDevice),
+                "bf16 weights upload");
+        e.w_base = base;
+        e.w_floats = host.size();
+        e.w_h = static_cast<const uint16_t *>(e.weights_h.p);
+    }
     size_t oi = 0;
     auto nxt = [&]() { return base + offs[oi++]; };
     e.emb = nxt();

@@ -19,7 +19,16 @@
 // Epilogues fused into the store: + bias[n], tanh / sigmoid, + residual, and
 // the paired SiLU gate of the FFN (W rows interleaved in blocks of 32 "in"
 // then 32 "gate" rows; output silu(in) * gate).
+//
+// bf16 weights (GemmParams::Wh, the C5 configuration's weight type): the
+// large-tile and decode kernels take a WB flag.  W streams as bf16, A stays
+// fp32 in memory and is rounded to bf16 (round to nearest even, the gfx950
+// v_cvt_pk_bf16_f32) as it enters the matrix core; products accumulate in fp32
+// with v_mfma_f32_16x16x32_bf16 (lane l: A[m = l % 16][k = 8 (l / 16) + j],
+// B[k = 8 (l / 16) + j][n = l % 16], j < 8; accumulator layout as for
+// v_mfma_f32_16x16x4f32), so the epilogues are shared.  Needs K % 8 == 0.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -204,6 +213,18 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmGroup g, int per
 // for lane group g on both operands).
 // ---------------------------------------------------------------------------
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Eight fp32 values (k order) rounded to bf16 for one MFMA operand.
+__device__ __forceinline__ bf16x8 to_bf16x8(floatx4 lo, floatx4 hi) {
+    bf16x8 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        r[q] = (__bf16)lo[q];
+        r[4 + q] = (__bf16)hi[q];
+    }
+    return r;
+}
 constexpr int kBigBM = 256, kBigThreads = 512;
 // K tile: 32 where the accumulators leave room for the larger load set, else 16.
 template <int BN> constexpr int big_bk() { return BN >= 256 ? 16 : 32; }
@@ -238,6 +259,53 @@ __device__ __forceinline__ void big_store(const BigLoad<ROWS, BK> &t, float *lds
     }
 }
 
+// bf16 tiles of the WB path: rows of 32 k (64 bytes) padded to kLdh = 40
+// elements (80 bytes) in LDS.
+constexpr int kLdh = 40;
+
+template <int ROWS>
+struct BigLoadH {
+    static constexpr int kChunks = ROWS * 4;                               // 16-byte runs per tile
+    static constexpr int kPer = (kChunks + kBigThreads - 1) / kBigThreads;  // per thread
+    floatx4 v[kPer];                                                        // raw bf16 bits
+};
+
+template <int ROWS>
+__device__ __forceinline__ void big_load_h(BigLoadH<ROWS> &t, __amdgpu_buffer_rsrc_t rsrc, int ld, int k0, int K,
+                                           int tid) {
+#pragma unroll
+    for (int i = 0; i < BigLoadH<ROWS>::kPer; ++i) {
+        const int q = tid + i * kBigThreads;
+        const int row = q / 4, k = k0 + (q % 4) * 8;
+        // K % 8 == 0 on this path: a run of 8 is wholly inside or outside [0, K).
+        const uint32_t off = (q < BigLoadH<ROWS>::kChunks && k < K) ? (uint32_t)((size_t)row * ld + k) * 2u : kBufferOob;
+        t.v[i] = __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0, 0));
+    }
+}
+
+template <int ROWS>
+__device__ __forceinline__ void big_store_h(const BigLoadH<ROWS> &t, __bf16 *lds, int tid) {
+#pragma unroll
+    for (int i = 0; i < BigLoadH<ROWS>::kPer; ++i) {
+        const int q = tid + i * kBigThreads;
+        if (q < BigLoadH<ROWS>::kChunks) *reinterpret_cast<floatx4 *>(lds + (q / 4) * kLdh + (q % 4) * 8) = t.v[i];
+    }
+}
+
+// fp32 A tile (32 k) rounded to bf16 on its way into LDS.
+template <int ROWS>
+__device__ __forceinline__ void big_store_a_h(const BigLoad<ROWS, 32> &t, __bf16 *lds, int tid) {
+    typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int i = 0; i < BigLoad<ROWS, 32>::kPer; ++i) {
+        const int q = tid + i * kBigThreads;
+        if (q < BigLoad<ROWS, 32>::kF4) {
+            const bf16x4 h = {(__bf16)t.v[i].x, (__bf16)t.v[i].y, (__bf16)t.v[i].z, (__bf16)t.v[i].w};
+            *reinterpret_cast<bf16x4 *>(lds + (q / 8) * kLdh + (q % 8) * 4) = h;
+        }
+    }
+}
+
 // Epilogue of the large-tile path through LDS: 16 accumulator rows of a wave at
 // a time are written to LDS and read back row-contiguous, so every global
 // access (C, residual, bias) is a 16-byte run along a row.  Needs 16-byte
@@ -247,13 +315,17 @@ __device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4
     return *reinterpret_cast<const float4 *>(stage + row * (WN + 4) + 4 * c4);
 }
 
-template <int BN, bool STAGED>
+template <int BN, bool STAGED, bool WB>
 __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int per_xcd) {
     constexpr int WN = BN / 2, NT = WN / 16;
-    constexpr int kBigBK = big_bk<BN>(), kBigLd = kBigBK + 4;
-    __shared__ __attribute__((aligned(16))) float lds[2 * (kBigBM + BN) * kBigLd];
+    constexpr int kBigBK = WB ? 32 : big_bk<BN>(), kBigLd = kBigBK + 4;
+    constexpr int kLdsFloats = WB ? (2 * (kBigBM + BN) * kLdh) / 2 : 2 * (kBigBM + BN) * kBigLd;
+    static_assert(kLdsFloats >= kBigThreads / 64 * 16 * (WN + 4), "LDS too small for the staged epilogue");
+    __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
     float(*As)[kBigBM * kBigLd] = reinterpret_cast<float(*)[kBigBM * kBigLd]>(lds);
     float(*Bs)[BN * kBigLd] = reinterpret_cast<float(*)[BN * kBigLd]>(lds + 2 * kBigBM * kBigLd);
+    __bf16 *Ah = reinterpret_cast<__bf16 *>(lds);  // WB: [2][kBigBM * kLdh], then [2][BN * kLdh]
+    __bf16 *Bh = Ah + 2 * kBigBM * kLdh;
 
     const GemmParams &p = g.p[blockIdx.y];
     const int tiles_n = g.tiles_n[blockIdx.y];
@@ -267,7 +339,8 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
     const int g4 = lane >> 4, li = lane & 15;
     const int rows_a = min(kBigBM, p.M - m0), rows_w = min(BN, p.N - n0);
     const auto ra = make_rsrc(p.A + (size_t)m0 * p.lda, (uint32_t)(((size_t)(rows_a - 1) * p.lda + p.K) * 4));
-    const auto rw = make_rsrc(p.W + (size_t)n0 * p.ldw, (uint32_t)(((size_t)(rows_w - 1) * p.ldw + p.K) * 4));
+    const auto rw = WB ? make_rsrc(p.Wh + (size_t)n0 * p.ldw, (uint32_t)(((size_t)(rows_w - 1) * p.ldw + p.K) * 2))
+                       : make_rsrc(p.W + (size_t)n0 * p.ldw, (uint32_t)(((size_t)(rows_w - 1) * p.ldw + p.K) * 4));
 
     floatx4 acc[4][NT];
 #pragma unroll
@@ -277,11 +350,23 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
 
     const int k_tiles = (p.K + kBigBK - 1) / kBigBK;
     BigLoad<kBigBM, kBigBK> ta;
-    BigLoad<BN, kBigBK> tb;
+    std::conditional_t<WB, BigLoadH<BN>, BigLoad<BN, kBigBK>> tb;
+    auto load_w = [&](int k0) {
+        if constexpr (WB) big_load_h(tb, rw, p.ldw, k0, p.K, tid);
+        else big_load(tb, rw, p.ldw, k0, p.K, tid);
+    };
+    auto store_tiles = [&](int buf) {
+        if constexpr (WB) {
+            big_store_a_h(ta, Ah + buf * kBigBM * kLdh, tid);
+            big_store_h(tb, Bh + buf * BN * kLdh, tid);
+        } else {
+            big_store(ta, As[buf], tid);
+            big_store(tb, Bs[buf], tid);
+        }
+    };
     big_load(ta, ra, p.lda, 0, p.K, tid);
-    big_load(tb, rw, p.ldw, 0, p.K, tid);
-    big_store(ta, As[0], tid);
-    big_store(tb, Bs[0], tid);
+    load_w(0);
+    store_tiles(0);
     lds_barrier();
 
     for (int kt = 0; kt < k_tiles; ++kt) {
@@ -289,10 +374,24 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
         const bool more = kt + 1 < k_tiles;
         if (more) {
             big_load(ta, ra, p.lda, (kt + 1) * kBigBK, p.K, tid);
-            big_load(tb, rw, p.ldw, (kt + 1) * kBigBK, p.K, tid);
+            load_w((kt + 1) * kBigBK);
+        }
+        if constexpr (WB) {
+            // One 32-k step: a lane's 8 k of a row are one ds_read_b128.
+            const __bf16 *Ac = Ah + cur * kBigBM * kLdh, *Bc = Bh + cur * BN * kLdh;
+            bf16x8 af[4], bf[NT];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(Ac + (wm * 64 + i * 16 + li) * kLdh + 8 * g4);
+#pragma unroll
+            for (int j = 0; j < NT; ++j) bf[j] = *reinterpret_cast<const bf16x8 *>(Bc + (wn * WN + j * 16 + li) * kLdh + 8 * g4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
         }
 #pragma unroll
-        for (int h = 0; h < kBigBK / 16; ++h) {  // 16 k per half: one ds_read_b128 per operand fragment
+        for (int h = 0; h < (WB ? 0 : kBigBK / 16); ++h) {  // 16 k per half: one ds_read_b128 per operand fragment
             floatx4 af[4], bf[NT];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -308,10 +407,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
                     for (int j = 0; j < NT; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][r], bf[j][r], acc[i][j], 0, 0, 0);
         }
-        if (more) {
-            big_store(ta, As[cur ^ 1], tid);
-            big_store(tb, Bs[cur ^ 1], tid);
-        }
+        if (more) store_tiles(cur ^ 1);
         lds_barrier();
     }
 
@@ -461,17 +557,22 @@ struct DecodeGroup {
     int count, units, per_xcd;
 };
 
-// Largest S (16-k steps in flight per wave) that keeps the prefetched operands
+// Largest S (k steps in flight per wave) that keeps the prefetched operands
 // within the register budget of a 1024-thread workgroup (128 VGPRs per lane).
-constexpr int dec_cap(int NT, int MI, int PRO) {
-    return MI == 1 ? (NT == 1 && PRO < 2 ? 10 : 6) : (NT == 1 ? (PRO == 0 ? 4 : 3) : 3);
+// A WB step covers 32 k and holds 8 A floats per m-tile (4 for fp32 W).
+constexpr int dec_cap(int NT, int MI, int PRO, bool WB = false) {
+    const int c = MI == 1 ? (NT == 1 && PRO < 2 ? 10 : 6) : (NT == 1 ? (PRO == 0 ? 4 : 3) : 3);
+    return WB ? (c >= 6 ? c - 4 : c - 1) : c;
 }
 
 // MULTI = false: a single product, whose parameters sit at fixed kernel-argument
 // offsets (no dependent argument load to find the product of a unit).
-template <int NT, int MI, int S, int PRO, bool MULTI>
+template <int NT, int MI, int S, int PRO, bool MULTI, bool WB>
 __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g) {
     constexpr int RT = 16 * MI;  // rows per workgroup
+    constexpr int KS = WB ? 32 : 16;  // k per step
+    constexpr int RL = KS / 4;        // consecutive k per lane and step
+    constexpr int AH = RL / 4;        // floatx4 per lane, m-tile and step
     __shared__ __attribute__((aligned(16))) float red[kDecWaves][NT][RT * 17];
     __shared__ float stats[PRO > 0 ? RT : 1][2];
     __shared__ float part[2][PRO > 0 ? kDecWaves : 1][PRO > 0 ? RT : 1];  // per-wave row partial sums
@@ -496,18 +597,19 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: k ranges and step guards are scalar
     const int g4 = lane >> 4, li = lane & 15;
-    const int spw = ((p.K + 15) / 16 + kDecWaves - 1) / kDecWaves;  // 16-k steps per wave
-    const int k_begin = min(p.K, wave * spw * 16), k_end = min(p.K, k_begin + spw * 16);
+    const int spw = ((p.K + KS - 1) / KS + kDecWaves - 1) / kDecWaves;  // k steps per wave
+    const int k_begin = min(p.K, wave * spw * KS), k_end = min(p.K, k_begin + spw * KS);
     const auto ra = make_rsrc(p.A + (size_t)row0 * p.lda, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
-    const auto rw = make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 4));
+    const auto rw = WB ? make_rsrc(p.Wh, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 2))
+                       : make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 4));
 
     floatx4 acc[NT][MI];
 #pragma unroll
     for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int i = 0; i < MI; ++i) acc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    floatx4 a[S][MI], b[S][NT];
-    floatx4 gt[PRO == 2 ? S : 1][MI];
+    floatx4 a[S][MI][AH], b[S][NT];  // b: 4 fp32 W values, or 8 bf16 ones (raw bits)
+    floatx4 gt[PRO == 2 ? S : 1][MI][AH];
     auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
@@ -516,20 +618,24 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
                                   PRO == 2 ? (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4) : 0u);
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const int k = k0 + 16 * s + 4 * g4;
-            const bool kin = k < k_end;  // K % 4 == 0 on this path
+            const int k = k0 + KS * s + RL * g4;
+            const bool kin = k < k_end;  // K % RL == 0 on this path
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 const int wr = w_row0 + 32 * t + li;
-                b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob);
+                b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * (WB ? 2u : 4u) : kBufferOob);
             }
 #pragma unroll
             for (int i = 0; i < MI; ++i)
-                a[s][i] = load4(ra, kin ? (uint32_t)((size_t)(16 * i + li) * p.lda + k) * 4u : kBufferOob);
+#pragma unroll
+                for (int hh = 0; hh < AH; ++hh)
+                    a[s][i][hh] = load4(ra, kin ? (uint32_t)((size_t)(16 * i + li) * p.lda + k + 4 * hh) * 4u : kBufferOob);
             if constexpr (PRO == 2) {
 #pragma unroll
                 for (int i = 0; i < MI; ++i)
-                    gt[s][i] = load4(rt, kin ? (uint32_t)((size_t)(16 * i + li) * p.ldg + k) * 4u : kBufferOob);
+#pragma unroll
+                    for (int hh = 0; hh < AH; ++hh)
+                        gt[s][i][hh] = load4(rt, kin ? (uint32_t)((size_t)(16 * i + li) * p.ldg + k + 4 * hh) * 4u : kBufferOob);
             }
         }
     };
@@ -552,7 +658,9 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
             for (int i = 0; i < MI; ++i) {
                 ps[i] = 0.0f;
 #pragma unroll
-                for (int s = 0; s < S; ++s) ps[i] += (a[s][i][0] + a[s][i][1]) + (a[s][i][2] + a[s][i][3]);
+                for (int s = 0; s < S; ++s)
+#pragma unroll
+                    for (int hh = 0; hh < AH; ++hh) ps[i] += (a[s][i][hh][0] + a[s][i][hh][1]) + (a[s][i][hh][2] + a[s][i][hh][3]);
                 ps[i] += __shfl_xor(ps[i], 16);
                 ps[i] += __shfl_xor(ps[i], 32);
                 if (g4 == 0) part[0][wave][16 * i + li] = ps[i];
@@ -567,12 +675,14 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
                 float sq = 0.0f;
 #pragma unroll
                 for (int s = 0; s < S; ++s) {
-                    if (k_begin + 16 * s + 4 * g4 < k_end) {
+                    if (k_begin + KS * s + RL * g4 < k_end) {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const float dv = a[s][i][q] - mean[i];
-                            sq = fmaf(dv, dv, sq);
-                        }
+                        for (int hh = 0; hh < AH; ++hh)
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const float dv = a[s][i][hh][q] - mean[i];
+                                sq = fmaf(dv, dv, sq);
+                            }
                     }
                 }
                 sq += __shfl_xor(sq, 16);
@@ -624,9 +734,11 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
     for (int k0 = k_begin;;) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            if (k0 + 16 * s >= k_end) break;  // steps past this wave's K range: no MFMAs on zeros
+            if (k0 + KS * s >= k_end) break;  // steps past this wave's K range: no MFMAs on zeros
             if constexpr (PRO > 0) {
-                const int k = k0 + 16 * s + 4 * g4;
+#pragma unroll
+                for (int hh = 0; hh < AH; ++hh) {
+                const int k = k0 + KS * s + RL * g4 + 4 * hh;
                 if (k < k_end) {
                     const floatx4 gm = *reinterpret_cast<const floatx4 *>(affine + k);
                     const floatx4 bt = *reinterpret_cast<const floatx4 *>(affine + 64 * kDecLnPerLane + k);
@@ -634,21 +746,32 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
                     for (int i = 0; i < MI; ++i)
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
-                            float y = (a[s][i][q] - mean[i]) * rstd[i] * gm[q] + bt[q];
-                            if constexpr (PRO == 2) y *= gt[s][i][q];
-                            a[s][i][q] = y;
+                            float y = (a[s][i][hh][q] - mean[i]) * rstd[i] * gm[q] + bt[q];
+                            if constexpr (PRO == 2) y *= gt[s][i][hh][q];
+                            a[s][i][hh][q] = y;
                         }
                 }
+                }
             }
+            if constexpr (WB) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
+                for (int i = 0; i < MI; ++i) {
+                    const bf16x8 ah = to_bf16x8(a[s][i][0], a[s][i][AH - 1]);
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
+                    for (int t = 0; t < NT; ++t)
+                        acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, __builtin_bit_cast(bf16x8, b[s][t]), acc[t][i], 0, 0, 0);
+                }
+            } else {
 #pragma unroll
-                    for (int i = 0; i < MI; ++i)
-                        acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s][i][r], b[s][t][r], acc[t][i], 0, 0, 0);
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int i = 0; i < MI; ++i)
+                            acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s][i][0][r], b[s][t][r], acc[t][i], 0, 0, 0);
+            }
         }
-        k0 += 16 * S;
+        k0 += KS * S;
         if (k0 >= k_end) break;
         load_round(k0);
     }
@@ -842,33 +965,52 @@ __global__ void gemm_splitk_reduce_kernel(GemmParams p, int splits) {
     }
 }
 
-template <int BN>
+template <int BN, bool WB>
 void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStream_t stream) {
     if (staged)
-        hipLaunchKernelGGL((gemm_big_kernel<BN, true>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+        hipLaunchKernelGGL((gemm_big_kernel<BN, true, WB>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
     else
-        hipLaunchKernelGGL((gemm_big_kernel<BN, false>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+        hipLaunchKernelGGL((gemm_big_kernel<BN, false, WB>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
 }
 
-template <int NT, int MI, int PRO, int S>
+template <int NT, int MI, int PRO, bool WB, int S>
 void launch_dec_s(const DecodeGroup &g, dim3 grid, hipStream_t stream) {
-    if constexpr (S <= dec_cap(NT, MI, PRO)) {
+    if constexpr (S <= dec_cap(NT, MI, PRO, WB)) {
         if (g.count == 1)
-            hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO, false>), grid, dim3(kDecThreads), 0, stream, g);
+            hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO, false, WB>), grid, dim3(kDecThreads), 0, stream, g);
         else if constexpr (PRO == 0)
-            hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO, true>), grid, dim3(kDecThreads), 0, stream, g);
+            hipLaunchKernelGGL((gemm_decode_kernel<NT, MI, S, PRO, true, WB>), grid, dim3(kDecThreads), 0, stream, g);
     }
 }
 
-template <int NT, int MI, int PRO>
+template <int NT, int MI, int PRO, bool WB>
 void launch_dec(const DecodeGroup &g, int S, dim3 grid, hipStream_t stream) {
     switch (S) {
-        case 1: launch_dec_s<NT, MI, PRO, 1>(g, grid, stream); break;
-        case 2: launch_dec_s<NT, MI, PRO, 2>(g, grid, stream); break;
-        case 3: launch_dec_s<NT, MI, PRO, 3>(g, grid, stream); break;
-        case 4: launch_dec_s<NT, MI, PRO, 4>(g, grid, stream); break;
-        case 6: launch_dec_s<NT, MI, PRO, 6>(g, grid, stream); break;
-        default: launch_dec_s<NT, MI, PRO, 10>(g, grid, stream); break;
+        case 1: launch_dec_s<NT, MI, PRO, WB, 1>(g, grid, stream); break;
+        case 2: launch_dec_s<NT, MI, PRO, WB, 2>(g, grid, stream); break;
+        case 3: launch_dec_s<NT, MI, PRO, WB, 3>(g, grid, stream); break;
+        case 4: launch_dec_s<NT, MI, PRO, WB, 4>(g, grid, stream); break;
+        case 6: launch_dec_s<NT, MI, PRO, WB, 6>(g, grid, stream); break;
+        default: launch_dec_s<NT, MI, PRO, WB, 10>(g, grid, stream); break;
+    }
+}
+
+template <bool WB>
+void launch_dec_kind(const DecodeGroup &g, int NT, int MI, int PRO, int S, dim3 grid, hipStream_t stream) {
+    if (PRO == 0) {
+        if (NT == 1) {
+            if (MI == 1) launch_dec<1, 1, 0, WB>(g, S, grid, stream);
+            else launch_dec<1, 4, 0, WB>(g, S, grid, stream);
+        } else {
+            if (MI == 1) launch_dec<2, 1, 0, WB>(g, S, grid, stream);
+            else launch_dec<2, 4, 0, WB>(g, S, grid, stream);
+        }
+    } else if (PRO == 1) {
+        if (NT == 2) launch_dec<2, 1, 1, WB>(g, S, grid, stream);
+        else if (MI == 1) launch_dec<1, 1, 1, WB>(g, S, grid, stream);
+        else launch_dec<1, 4, 1, WB>(g, S, grid, stream);
+    } else {
+        launch_dec<1, 1, 2, WB>(g, S, grid, stream);
     }
 }
 
@@ -882,11 +1024,14 @@ int pick_steps(int spw, int cap) {
 
 int dec_prologue(const GemmParams &p) { return p.ln_gamma ? (p.a_gate ? 2 : 1) : 0; }
 
-// Decode products (M <= 64, K % 4 == 0): one launch per group; all products of
-// a group share the SiLU-pair flag and the prologue kind.
+// Decode products (M <= 64, K % 4 == 0; K % 8 == 0 for bf16 W): one launch per
+// group; all products of a group share the SiLU-pair flag, the prologue kind
+// and the weight type.
 hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
     if (count < 1 || count > kMaxDecode) return hipErrorInvalidValue;
     const int NT = ps[0].silu_pair ? 2 : 1, PRO = dec_prologue(ps[0]);
+    const bool WB = ps[0].Wh != nullptr;
+    const int KS = WB ? 32 : 16;
     if (PRO > 0 && count > 1) {  // grouped launches exist for plain products only
         for (int i = 0; i < count; ++i) {
             const hipError_t e = launch_decode(ps + i, 1, stream);
@@ -899,7 +1044,7 @@ hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
         const GemmParams &p = ps[i];
         const int slices = p.silu_pair ? p.N / 32 : (p.N + 15) / 16;
         units1 += slices * ((p.M + 15) / 16);
-        spw = std::max(spw, ((p.K + 15) / 16 + kDecWaves - 1) / kDecWaves);
+        spw = std::max(spw, ((p.K + KS - 1) / KS + kDecWaves - 1) / kDecWaves);
     }
     // Wide products (the LM head) already fill the chip with 64-row tiles.
     const int MI = (units1 > 1024 && PRO < 2 && !(PRO == 1 && NT == 2)) ? 4 : 1;
@@ -915,28 +1060,15 @@ hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
     }
     g.per_xcd = (g.units + kXcds - 1) / kXcds;
     const dim3 grid(g.per_xcd * kXcds);
-    const int cap = dec_cap(NT, MI, PRO);
+    const int cap = dec_cap(NT, MI, PRO, WB);
     const int S = pick_steps(spw, cap);
-    if (PRO == 0) {
-        if (NT == 1) {
-            if (MI == 1) launch_dec<1, 1, 0>(g, S, grid, stream);
-            else launch_dec<1, 4, 0>(g, S, grid, stream);
-        } else {
-            if (MI == 1) launch_dec<2, 1, 0>(g, S, grid, stream);
-            else launch_dec<2, 4, 0>(g, S, grid, stream);
-        }
-    } else if (PRO == 1) {
-        if (NT == 2) launch_dec<2, 1, 1>(g, S, grid, stream);
-        else if (MI == 1) launch_dec<1, 1, 1>(g, S, grid, stream);
-        else launch_dec<1, 4, 1>(g, S, grid, stream);
-    } else {
-        if (NT == 2) return hipErrorInvalidValue;
-        launch_dec<1, 1, 2>(g, S, grid, stream);
-    }
+    if (PRO == 2 && NT == 2) return hipErrorInvalidValue;
+    if (WB) launch_dec_kind<true>(g, NT, MI, PRO, S, grid, stream);
+    else launch_dec_kind<false>(g, NT, MI, PRO, S, grid, stream);
     return hipGetLastError();
 }
 
-bool decode_ok(const GemmParams &p) { return p.M <= 64 && p.K % 4 == 0; }
+bool decode_ok(const GemmParams &p) { return p.M <= 64 && p.K % (p.Wh ? 8 : 4) == 0; }
 
 // The A-side prologue exists on the decode path only, for K <= 1024.
 bool prologue_ok(const GemmParams &p) {
@@ -963,6 +1095,7 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
     if (!prologue_ok(p)) return hipErrorInvalidValue;
     if (decode_ok(p)) return launch_decode(&p, 1, stream);
+    if (p.Wh) return launch_gemm_group(&p, 1, stream);  // bf16 W: large-tile path or an error
     if (p.M <= 64) {
         int splits = skinny_splits(p.N, p.K);
         if (!p.workspace || (size_t)splits * p.M * p.N > p.workspace_floats) splits = 1;
@@ -986,29 +1119,71 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
     for (int i = 0; i < count; ++i)
         if (ps[i].M > 0 && ps[i].N > 0 && !prologue_ok(ps[i])) return hipErrorInvalidValue;
     {
-        // Decode-shaped products: one launch per (SiLU flag, prologue kind).
-        GemmParams dec[6][kMaxGroup];
-        int nd[6] = {0, 0, 0, 0, 0, 0};
+        // Decode-shaped products: one launch per (SiLU flag, prologue kind, W type).
+        GemmParams dec[12][kMaxGroup];
+        int nd[12] = {};
         for (int i = 0; i < count; ++i) {
             const GemmParams &p = ps[i];
             if (p.M <= 0 || p.N <= 0 || !decode_ok(p)) continue;
             if (p.K <= 0 || p.lda < p.K || p.ldw < p.K) return hipErrorInvalidValue;
             if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
-            const int key = (p.silu_pair ? 3 : 0) + dec_prologue(p);
+            const int key = (p.Wh ? 6 : 0) + (p.silu_pair ? 3 : 0) + dec_prologue(p);
             dec[key][nd[key]++] = p;
         }
-        for (int f = 0; f < 6; ++f)
+        for (int f = 0; f < 12; ++f)
             if (nd[f] > 0) {
                 hipError_t e = launch_decode(dec[f], nd[f], stream);
                 if (e != hipSuccess) return e;
             }
+    }
+    // bf16-weight products: the large-tile kernel for any M, or an error.
+    {
+        GemmGroup gh{};
+        int nh = 0, hmax = 0;
+        bool f256 = true, f160 = true, f128 = true, f64 = true;
+        for (int i = 0; i < count; ++i) {
+            const GemmParams &p = ps[i];
+            if (p.M <= 0 || p.N <= 0 || !p.Wh || decode_ok(p)) continue;
+            if (p.K <= 0 || p.K % 8 != 0 || p.lda < p.K || p.ldw < p.K) return hipErrorInvalidValue;
+            if (p.silu_pair && (p.N % 64) != 0) return hipErrorInvalidValue;
+            if ((size_t)kBigBM * p.lda * 4 >= (1u << 31) || (size_t)256 * p.ldw * 2 >= (1u << 31)) return hipErrorInvalidValue;
+            f256 = f256 && p.N % 256 == 0;
+            f160 = f160 && p.N % 160 == 0 && !p.silu_pair;
+            f128 = f128 && p.N % 128 == 0;
+            f64 = f64 && p.N % 64 == 0 && !p.silu_pair;
+            gh.p[nh++] = p;
+        }
+        if (nh > 0) {
+            if (!(f256 || f160 || f128 || f64)) return hipErrorInvalidValue;
+            const int bn = f256 ? 256 : f160 ? 160 : f128 ? 128 : 64;
+            bool staged = true;
+            for (int i = 0; i < nh; ++i) {
+                const GemmParams &p = gh.p[i];
+                gh.tiles_n[i] = p.N / bn;
+                gh.total[i] = ((p.M + kBigBM - 1) / kBigBM) * gh.tiles_n[i];
+                hmax = std::max(hmax, gh.total[i]);
+                const uintptr_t bits = reinterpret_cast<uintptr_t>(p.C) | reinterpret_cast<uintptr_t>(p.residual) |
+                                       reinterpret_cast<uintptr_t>(p.bias);
+                staged = staged && (bits & 15) == 0 && p.ldc % 4 == 0 && (!p.residual || p.ldr % 4 == 0);
+            }
+            const int per_xcd = (hmax + kXcds - 1) / kXcds;
+            const dim3 grid(per_xcd * kXcds, nh);
+            switch (bn) {
+                case 256: launch_big<256, true>(gh, per_xcd, staged, grid, stream); break;
+                case 160: launch_big<160, true>(gh, per_xcd, staged, grid, stream); break;
+                case 128: launch_big<128, true>(gh, per_xcd, staged, grid, stream); break;
+                default: launch_big<64, true>(gh, per_xcd, staged, grid, stream); break;
+            }
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
     }
     GemmGroup g{};
     int max_total = 0, n = 0;
     for (int i = 0; i < count; ++i) {
         const GemmParams &p = ps[i];
         if (p.M <= 0 || p.N <= 0) continue;
-        if (decode_ok(p)) continue;  // launched above
+        if (decode_ok(p) || p.Wh) continue;  // launched above
         if (p.M <= 64) {  // short-M products take the split-K path one by one
             hipError_t e = launch_gemm(p, stream);
             if (e != hipSuccess) return e;
@@ -1053,10 +1228,10 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
         }
         const dim3 grid(per_xcd * kXcds, n), block(kBigThreads);
 switch (bn) {
-            case 256: launch_big<256>(g, per_xcd, staged, grid, stream); break;
-            case 160: launch_big<160>(g, per_xcd, staged, grid, stream); break;
-            case 128: launch_big<128>(g, per_xcd, staged, grid, stream); break;
-            default: launch_big<64>(g, per_xcd, staged, grid, stream); break;
+            case 256: launch_big<256, false>(g, per_xcd, staged, grid, stream); break;
+            case 160: launch_big<160, false>(g, per_xcd, staged, grid, stream); break;
+            case 128: launch_big<128, false>(g, per_xcd, staged, grid, stream); break;
+            default: launch_big<64, false>(g, per_xcd, staged, grid, stream); break;
         }
         return hipGetLastError();
     }
@@ -1096,5 +1271,37 @@ extern "C" int yuf_ln_linear_f32(int M, int N, int K, const float *A, const floa
     p.ln_gamma = gamma; p.ln_beta = beta; p.a_gate = gate; p.ldg = gate ? K : 0;
     hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
     if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("ln_linear launch: ") + hipGetErrorString(err));
+    return YUF_OK;
+}
+
+extern "C" int yuf_linear_bf16w(int M, int N, int K, const float *A, const uint16_t *W, const float *bias, int act,
+                                const float *residual, float *C, void *stream) {
+    using namespace yuf;
+    if (M < 0 || N < 0 || K < 8 || K % 8 != 0) return fail(YUF_ERR_INVALID, "linear_bf16w: needs K % 8 == 0, K >= 8");
+    if (act < ACT_NONE || act > ACT_SIGMOID) return fail(YUF_ERR_INVALID, "linear_bf16w: bad activation");
+    if (M > 0 && N > 0 && (!A || !W || !C)) return fail(YUF_ERR_INVALID, "linear_bf16w: null pointer");
+    if (M > 64 && N % 64 != 0 && N % 160 != 0)
+        return fail(YUF_ERR_INVALID, "linear_bf16w: M > 64 needs N % 64 == 0 or N % 160 == 0");
+    GemmParams p;
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = K; p.Wh = W; p.ldw = K; p.C = C; p.ldc = N;
+    p.bias = bias; p.act = act; p.residual = residual; p.ldr = N;
+    hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("linear_bf16w launch: ") + hipGetErrorString(err));
+    return YUF_OK;
+}
+
+extern "C" int yuf_ln_linear_bf16w(int M, int N, int K, const float *A, const float *gamma, const float *beta,
+                                   const float *gate, const uint16_t *W, const float *bias, const float *residual,
+                                   float *C, void *stream) {
+    using namespace yuf;
+    if (M < 1 || M > 64 || N < 0 || K < 8 || K % 8 != 0 || K > 1024)
+        return fail(YUF_ERR_INVALID, "ln_linear_bf16w: needs 1 <= M <= 64, K % 8 == 0, 8 <= K <= 1024");
+    if (N > 0 && (!A || !gamma || !beta || !W || !C)) return fail(YUF_ERR_INVALID, "ln_linear_bf16w: null pointer");
+    GemmParams p;
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = K; p.Wh = W; p.ldw = K; p.C = C; p.ldc = N;
+    p.bias = bias; p.residual = residual; p.ldr = N;
+    p.ln_gamma = gamma; p.ln_beta = beta; p.a_gate = gate; p.ldg = gate ? K : 0;
+    hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("ln_linear_bf16w launch: ") + hipGetErrorString(err));
     return YUF_OK;
 }

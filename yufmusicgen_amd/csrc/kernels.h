@@ -67,6 +67,9 @@ struct GemmParams {
     int lda = 0;
     const float *W = nullptr;
     int ldw = 0;
+    // bf16 weights (raw bits, [N][ldw]) instead of W: the large-tile and decode
+    // kernels round A to bf16 and accumulate in fp32; needs K % 8 == 0.
+    const uint16_t *Wh = nullptr;
     float *C = nullptr;
     int ldc = 0;
     const float *bias = nullptr;      // [N] added before the activation

@@ -70,10 +70,18 @@ class Checkpoint:
 class Engine:
     """Device-resident weights and ``max_streams`` recurrent-state slots."""
 
-    def __init__(self, ckpt: Checkpoint, max_streams: int = 1, max_tokens: int = 4096):
+    WEIGHT_TYPES = {"f32": 0, "bf16": 1}
+
+    def __init__(self, ckpt: Checkpoint, max_streams: int = 1, max_tokens: int = 4096, weight_dtype: str = "f32"):
+        """``weight_dtype`` "bf16": bf16 projection weights with fp32 accumulation
+        (``yuf_engine_create_ex``); "f32" (default): everything fp32."""
+        if weight_dtype not in self.WEIGHT_TYPES:
+            raise ValueError(f"weight_dtype must be one of {sorted(self.WEIGHT_TYPES)}, got {weight_dtype!r}")
         handle = ctypes.c_void_p()
-        check(lib().yuf_engine_create(ckpt._h, int(max_streams), int(max_tokens), ctypes.byref(handle)))
+        check(lib().yuf_engine_create_ex(ckpt._h, int(max_streams), int(max_tokens),
+                                         self.WEIGHT_TYPES[weight_dtype], ctypes.byref(handle)))
         self._h = handle
+        self.weight_dtype = weight_dtype
         c = ModelConfigC()
         check(lib().yuf_engine_config(self._h, ctypes.byref(c)))
         self.config = _config_dict(c)
