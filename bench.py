@@ -22,6 +22,11 @@ In the same run:
     this host's cores (~10-30 s of CPU work).
 
 Only N = 1 GPU exists on these boxes; --gpus above 1 exits with a message.
+
+`--only c5` (not part of the default run): the C5 architecture (24 layers,
+d_model 1024, 16 x 64 heads, ROSA 256) with fp32 and with bf16 projection
+weights on a bounded slice of C5 (32 rows x 1024 tokens of prefill, last-position
+logits, then 64 decode steps of the 32 streams).
 """
 
 from __future__ import annotations
@@ -110,6 +115,58 @@ def bench_gemm(iters: int) -> dict:
             "avg_us": round(ms * 1e3, 1)}
 
 
+def bench_c5(args) -> dict:
+    """C5 architecture, fp32 vs bf16 projection weights, bounded slice."""
+    import torch
+
+    from yufmusicgen_amd.checkpoint import write_yuf
+    from yufmusicgen_amd.config import PRESETS
+    from yufmusicgen_amd.engine import Checkpoint, Engine
+    from yufmusicgen_amd.synth import prompt_tokens, synth_weights, uniform_tokens
+
+    cfg = PRESETS["wide"]
+    log("c5: generating weights")
+    weights = synth_weights(cfg, seed=0)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "c5.yuf")
+        write_yuf(path, cfg, weights)
+        ckpt = Checkpoint.load(path)
+    B, T, D = 32, 1024, 64
+    tokens = torch.from_numpy(prompt_tokens(0, B, T, cfg.vocab_size)).cuda()
+    step_tokens = torch.from_numpy(uniform_tokens(1, B, D, cfg.vocab_size)).cuda()
+    slots = np.arange(B, dtype=np.int32)
+    out = {"workload": f"C5 architecture (24L, d=1024, 16x64, ROSA 256), prefill {B}x{T} last logits, "
+                       f"then {D} decode steps of {B} streams"}
+    for wt in ("f32", "bf16"):
+        engine = Engine(ckpt, max_streams=B, max_tokens=B * T, weight_dtype=wt)
+        logits = torch.empty(B, cfg.vocab_size, device="cuda")
+        for _ in range(max(1, args.warmup)):
+            engine.reset_state()
+            engine.prefill_device(tokens, logits, slots, logits="last")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            engine.reset_state()
+            engine.prefill_device(tokens, logits, slots, logits="last")
+        torch.cuda.synchronize()
+        pf = (time.perf_counter() - t0) / args.steps
+        for t in range(3):
+            engine.step_device(step_tokens[:, t].contiguous(), logits, slots)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for t in range(D):
+            engine.step_device(step_tokens[:, t].contiguous(), logits, slots)
+        torch.cuda.synchronize()
+        dc = (time.perf_counter() - t0) / D
+        out[wt] = {"prefill_tokens_per_s": round(B * T / pf), "prefill_ms": round(pf * 1e3, 2),
+                   "decode_tokens_per_s": round(B / dc), "decode_ms_per_step": round(dc * 1e3, 3)}
+        log(f"c5 {wt}: prefill {pf * 1e3:.1f} ms ({B * T / pf:.0f} tok/s), decode {dc * 1e3:.3f} ms/step")
+        engine.close()
+        del engine
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(weights, cfg) -> dict:
     import torch
 
@@ -141,7 +198,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5"], default=None,
                     help="profiling aids: just the C2 scan (20 launches), just the prefill steps, just the C4 "
                          "decode leg, or a plain 256 MiB device copy (20 launches) that calibrates the "
                          "FETCH_SIZE/WRITE_SIZE counters")
@@ -167,6 +224,10 @@ def main() -> int:
     from yufmusicgen_amd.config import PRESETS
     from yufmusicgen_amd.engine import Checkpoint, Engine, sample_device
     from yufmusicgen_amd.synth import prompt_tokens, synth_weights, uniform_tokens
+
+    if args.only == "c5":
+        print(json.dumps({"c5": bench_c5(args)}), flush=True)
+        return 0
 
     cfg = PRESETS["0.1b"]
     log("generating weights")

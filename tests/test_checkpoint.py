@@ -89,7 +89,7 @@ def test_cpp_loader_rejects_malformed_files(tiny_yuf, tmp_path, case):
 
     mutate = {
         "magic": lambda d: b"NOPE" + d[4:],
-        "version": lambda d: d[:4] + struct.pack("<I", 2) + d[8:],
+        "version": lambda d: d[:4] + struct.pack("<I", 3) + d[8:],
         "truncated": lambda d: d[:-4],
         "extra": lambda d: d + b"\0\0\0\0",
         "json": lambda d: d[:16] + b"{" * 3 + d[19:],
@@ -111,3 +111,77 @@ def test_missing_file_is_io_error(tmp_path):
 def test_golden_fixture_loads(golden_dir):
     ck = Checkpoint.load(os.path.join(golden_dir, "model_state_test.yuf"))
     assert ck.config["d_model"] == 32 and ck.config["n_layers"] == 2
+
+
+# ----------------------------------------------------------------- version 2
+def _bf16_round(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32)
+    return r.view(np.float32)
+
+
+@pytest.fixture(scope="module")
+def bf16_yuf(tmp_path_factory):
+    cfg = PRESETS["state_test"]
+    path = tmp_path_factory.mktemp("ck2") / "bf16.yuf"
+    weights = synth_weights(cfg, seed=4)
+    write_yuf(path, cfg, weights, linear_bf16=True)
+    return path, cfg, weights
+
+
+def test_v2_bf16_roundtrip_python_and_cpp(bf16_yuf):
+    """nn.Linear weights stored as bf16 (round to nearest even, checked against
+    the bit-level rule), everything else f32 and unchanged, in both readers."""
+    path, cfg, weights = bf16_yuf
+    header, tensors = read_yuf(path)
+    assert header["version"] == 2 and struct.unpack("<I", path.read_bytes()[4:8])[0] == 2
+    kinds = {t["name"]: t["dtype"] for t in header["tensors"]}
+    assert kinds["blocks.0.time_mix.receptance.weight"] == "bf16" and kinds["blocks.0.ffn_in.weight"] == "bf16"
+    assert kinds["token_embedding.weight"] == "f32" and kinds["blocks.0.time_mix.k_k"] == "f32"
+    for t in header["tensors"]:
+        assert t["offset"] % (2 if t["dtype"] == "bf16" else 4) == 0
+    ck = Checkpoint.load(path)
+    for name, value in weights.items():
+        expect = _bf16_round(value) if kinds[name] == "bf16" else np.asarray(value, dtype=np.float32)
+        np.testing.assert_array_equal(tensors[name], expect)
+        np.testing.assert_array_equal(ck.tensor(name), expect)
+    # bf16 tensors take half the bytes.
+    f32_bytes = sum(np.asarray(v).size for v in weights.values()) * 4
+    bf16_count = sum(np.asarray(weights[n]).size for n, k in kinds.items() if k == "bf16")
+    assert header["payload_bytes"] <= f32_bytes - 2 * bf16_count + 2 * len(weights)
+
+
+def test_v2_all_f32_stays_version_1(tmp_path):
+    cfg = PRESETS["state_test"]
+    path = tmp_path / "f.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=4), dtypes={})
+    assert read_yuf(path)[0]["version"] == 1
+
+
+@pytest.mark.parametrize("case", ["dtype", "misaligned", "payload", "outside", "no_payload_field"])
+def test_v2_loader_rejects_malformed_files(bf16_yuf, tmp_path, case):
+    path = bf16_yuf[0]
+    header_len = struct.unpack("<Q", path.read_bytes()[8:16])[0]
+
+    def rewrite_header(data, fn):
+        header = json.loads(bytes(data[16:16 + header_len]))
+        fn(header)
+        blob = json.dumps(header).encode()
+        return data[:8] + struct.pack("<Q", len(blob)) + blob + data[16 + header_len:]
+
+    def first_bf16(h):
+        return next(t for t in h["tensors"] if t["dtype"] == "bf16")
+
+    mutate = {
+        "dtype": lambda d: rewrite_header(d, lambda h: first_bf16(h).update(dtype="f16")),
+        "misaligned": lambda d: rewrite_header(d, lambda h: first_bf16(h).update(offset=first_bf16(h)["offset"] + 1)),
+        "payload": lambda d: d[:-2],
+        "outside": lambda d: rewrite_header(d, lambda h: h["tensors"][-1].update(offset=h["payload_bytes"])),
+        "no_payload_field": lambda d: rewrite_header(d, lambda h: h.pop("payload_bytes")),
+    }[case]
+    bad = _corrupt(path, tmp_path, mutate)
+    with pytest.raises(YufError) as err:
+        Checkpoint.load(bad)
+    assert err.value.status == -3, str(err.value)
+    with pytest.raises((ValueError, KeyError)):
+        read_yuf(bad)

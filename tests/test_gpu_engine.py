@@ -235,6 +235,30 @@ def test_bf16_weights_engine_vs_bf16_oracle(tmp_path):
         assert dev <= 0.5 * effect, (name, dev, effect)
 
 
+def test_bf16_checkpoint_equals_rounded_f32_checkpoint(tmp_path):
+    """A version-2 .yuf with bf16 nn.Linear weights and the f32 .yuf of the same
+    weights give bit-identical logits and states in bf16 mode (the engine's
+    bf16 copies are the same values); in f32 mode the bf16 file runs its
+    widened weights, so it differs from the f32 file."""
+    import dataclasses
+    cfg = dataclasses.replace(PRESETS["0.1b"], n_layers=2)
+    weights = synth_weights(cfg, seed=9)
+    p32, p16 = tmp_path / "f32.yuf", tmp_path / "bf16.yuf"
+    write_yuf(p32, cfg, weights)
+    write_yuf(p16, cfg, weights, linear_bf16=True)
+    tokens = uniform_tokens(10, 2, 96, cfg.vocab_size)
+    outs = {}
+    for name, path, wt in (("f32file-bf16", p32, "bf16"), ("bf16file-bf16", p16, "bf16"),
+                           ("f32file-f32", p32, "f32"), ("bf16file-f32", p16, "f32")):
+        eng = Engine(Checkpoint.load(path), max_streams=2, max_tokens=192, weight_dtype=wt)
+        logits = eng.prefill(tokens, logits="all")
+        step = eng.step(tokens[:, 0])
+        outs[name] = (logits, step, _states_from_blob(eng, [0, 1]))
+    for a, b in zip(outs["f32file-bf16"], outs["bf16file-bf16"]):
+        np.testing.assert_array_equal(a, b)
+    assert np.abs(outs["f32file-f32"][0] - outs["bf16file-f32"][0]).max() > 0
+
+
 def test_rosa_segmented_prefill_matches_sequential(tmp_path, monkeypatch):
     """The segmented ROSA prefill (parallel 64-token segments around an A^64
     carry pass) against the sequential chunked scan, through the whole model:

@@ -3,7 +3,11 @@
 // Container (vulkan/scripts/export_checkpoint.py:32-146; checks of
 // vulkan/src/checkpoint.rs:90-149):
 //   b"YUFM" | u32 LE version = 1 | u64 LE header_len | UTF-8 JSON | f32 LE payload
-// The payload size must equal 4 * sum(tensors[].count) exactly.  The model
+// The payload size must equal 4 * sum(tensors[].count) exactly.
+// Version 2 (this build's extension for bf16 weights): tensor entries carry a
+// "dtype" ("f32" | "bf16") and a byte "offset" into the payload (a multiple of
+// the element size), the header a "payload_bytes" that the file size must
+// match; bf16 tensors are widened to f32 on load (exact).  The model
 // config is validated like ModelConfig::validate (checkpoint.rs:32-47) except
 // that the low-rank width is read from the w1 tensor's shape instead of the
 // Rust rounding formula, which disagrees with Python's at d_model = 1024.
@@ -216,7 +220,7 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
     unsigned char b4[4], b8[8];
     if (!f.read((char *)b4, 4)) return fail(YUF_ERR_FORMAT, "truncated header");
     version = b4[0] | (b4[1] << 8) | (b4[2] << 16) | ((uint32_t)b4[3] << 24);
-    if (version != 1) return fail(YUF_ERR_FORMAT, "unsupported .yuf version " + std::to_string(version));
+    if (version != 1 && version != 2) return fail(YUF_ERR_FORMAT, "unsupported .yuf version " + std::to_string(version));
     if (!f.read((char *)b8, 8)) return fail(YUF_ERR_FORMAT, "truncated header");
     for (int i = 7; i >= 0; --i) header_len = (header_len << 8) | b8[i];
     if (header_len > (uint64_t)file_len - 16) return fail(YUF_ERR_FORMAT, "header length exceeds file size");
@@ -258,6 +262,7 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
     const json::Value *tensors = root.get("tensors");
     if (!tensors || tensors->kind != json::Value::Array) return fail(YUF_ERR_FORMAT, "header has no tensors array");
     long long total = 0;
+    std::vector<std::pair<std::string, long long>> byte_offsets;  // version 2: payload byte offset per tensor
     for (const json::Value &t : tensors->arr) {
         TensorInfo info;
         const json::Value *name = t.get("name");
@@ -266,6 +271,16 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
         if (!name || name->kind != json::Value::String || !shape || shape->kind != json::Value::Array ||
             !get_int(&t, "offset", off) || !get_int(&t, "count", cnt) || off < 0 || cnt < 0)
             return fail(YUF_ERR_FORMAT, "malformed tensor entry in header");
+        if (version == 2) {
+            const json::Value *dt = t.get("dtype");
+            if (!dt || dt->kind != json::Value::String || (dt->str != "f32" && dt->str != "bf16"))
+                return fail(YUF_ERR_FORMAT, "tensor " + name->str + ": dtype must be \"f32\" or \"bf16\"");
+            info.bf16 = dt->str == "bf16";
+            if (off % (info.bf16 ? 2 : 4) != 0)
+                return fail(YUF_ERR_FORMAT, "tensor " + name->str + ": offset is not a multiple of its element size");
+            byte_offsets.emplace_back(name->str, off);
+            off = total;  // position in the widened f32 copy
+        }
         info.offset = off;
         info.count = cnt;
         long long prod = 1;
@@ -279,16 +294,47 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
         ck.tensors[name->str] = info;
     }
     const long long data_start = 16 + (long long)header_len;
-    const long long expected = data_start + total * 4;
-    if (file_len != expected)
-        return fail(YUF_ERR_FORMAT, "checkpoint size mismatch: file has " + std::to_string(file_len) +
-                                        " bytes, header expects " + std::to_string(expected));
-    for (const auto &kv : ck.tensors)
-        if (kv.second.offset + kv.second.count > total)
-            return fail(YUF_ERR_FORMAT, "tensor " + kv.first + " lies outside the payload");
-    ck.data.resize((size_t)total);
-    if (total > 0 && !f.read(reinterpret_cast<char *>(ck.data.data()), (std::streamsize)(total * 4)))
-        return fail(YUF_ERR_IO, "cannot read tensor payload");
+    if (version == 1) {
+        const long long expected = data_start + total * 4;
+        if (file_len != expected)
+            return fail(YUF_ERR_FORMAT, "checkpoint size mismatch: file has " + std::to_string(file_len) +
+                                            " bytes, header expects " + std::to_string(expected));
+        for (const auto &kv : ck.tensors)
+            if (kv.second.offset + kv.second.count > total)
+                return fail(YUF_ERR_FORMAT, "tensor " + kv.first + " lies outside the payload");
+        ck.data.resize((size_t)total);
+        if (total > 0 && !f.read(reinterpret_cast<char *>(ck.data.data()), (std::streamsize)(total * 4)))
+            return fail(YUF_ERR_IO, "cannot read tensor payload");
+    } else {
+        long long payload = -1;
+        if (!get_int(&root, "payload_bytes", payload) || payload < 0)
+            return fail(YUF_ERR_FORMAT, "version 2 header needs payload_bytes");
+        if (file_len != data_start + payload)
+            return fail(YUF_ERR_FORMAT, "checkpoint size mismatch: file has " + std::to_string(file_len) +
+                                            " bytes, header expects " + std::to_string(data_start + payload));
+        std::vector<unsigned char> raw((size_t)payload);
+        if (payload > 0 && !f.read(reinterpret_cast<char *>(raw.data()), (std::streamsize)payload))
+            return fail(YUF_ERR_IO, "cannot read tensor payload");
+        ck.data.resize((size_t)total);
+        for (const auto &no : byte_offsets) {
+            const TensorInfo &info = ck.tensors[no.first];
+            const long long width = info.bf16 ? 2 : 4;
+            if (no.second + width * info.count > payload)
+                return fail(YUF_ERR_FORMAT, "tensor " + no.first + " lies outside the payload");
+            float *dst = ck.data.data() + info.offset;
+            const unsigned char *src = raw.data() + no.second;
+            for (long long i = 0; i < info.count; ++i) {
+                uint32_t u;
+                if (info.bf16) {
+                    u = ((uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 8)) << 16;
+                } else {
+                    u = (uint32_t)src[4 * i] | ((uint32_t)src[4 * i + 1] << 8) | ((uint32_t)src[4 * i + 2] << 16) |
+                        ((uint32_t)src[4 * i + 3] << 24);
+                }
+                std::memcpy(dst + i, &u, 4);
+            }
+        }
+    }
 
     // Low-rank width from the w1 tensor ([d, L]).
     auto it = ck.tensors.find("blocks.0.time_mix.w1");

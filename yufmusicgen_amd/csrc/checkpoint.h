@@ -18,8 +18,9 @@ struct ModelShape {
 
 struct TensorInfo {
     std::vector<long long> dims;
-    long long offset = 0;  // in floats
+    long long offset = 0;  // in floats, into Checkpoint::data
     long long count = 0;
+    bool bf16 = false;  // stored as bf16 in the file (version 2); data holds it widened
 };
 
 struct Checkpoint {
