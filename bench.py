@@ -15,6 +15,8 @@ In the same run:
   * the WKV-7 scan (C2: B=8, T=2048, H=16, N=40, zero state) timed with HIP
     events on the stream it runs on -> `roofline` (algorithmic bytes / time
     against the 8 TB/s HBM peak);
+  * the single-token WKV-7 step of C4 and the ROSA scan of a C3 layer ->
+    `decode_roofline`, `rosa_roofline` (HBM, the same way);
   * the FFN in/gate projection GEMM of C3 (M=16384, N=5120, K=640) -> MFMA
     utilisation against the 157.3 TFLOP/s dense fp32 peak;
   * `cpu_baseline`: the oracle's float32 restatement of the reference's PyTorch
@@ -91,6 +93,59 @@ def bench_scan(iters: int) -> dict:
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "wkv7_chunk_kernel<3,false> (C2: B=8 T=2048 H=16 N=40)",
+            "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
+
+
+def bench_wkv_step(iters: int) -> dict:
+    """The single-token WKV-7 step of C4 (64 streams, H=16, N=40, state read and
+    written in place): 64 (2 H N^2 + 7 d) 4 bytes = 14.25 MB per layer-step."""
+    import torch
+
+    from yufmusicgen_amd._lib import check, lib
+    from yufmusicgen_amd.synth import wkv_inputs
+
+    B, H, N = 64, 16, 40
+    dev = [torch.from_numpy(x).cuda() for x in wkv_inputs(2, B, 1, H, N)]
+    y = torch.empty_like(dev[0])
+    state = torch.randn(B, H, N, N, device="cuda") * 0.1
+    st = torch.cuda.current_stream().cuda_stream
+    run = lambda: check(lib().yuf_wkv7_scan_f32(B, 1, H, N, *[x.data_ptr() for x in dev],  # noqa: E731
+                                                state.data_ptr(), state.data_ptr(), y.data_ptr(), st))
+    run()
+    torch.cuda.synchronize()
+    ms = time_events(run, iters, torch.cuda.current_stream())
+    nbytes = B * (2 * H * N * N + 7 * H * N) * 4
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "wkv7_step_kernel (C4: 64 streams, H=16, N=40, T=1)",
+            "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
+
+
+def bench_rosa(iters: int) -> dict:
+    """ROSA scan of one C3 layer (B=8, T=2048, D=128, gated read) through the
+    operator entry point (segmented form: A^64 on the device, segments from
+    zero, carry chain, segments again): 4 (4 B T D + 2 B D) bytes = 33.6 MB."""
+    import torch
+
+    from yufmusicgen_amd._lib import check, lib
+    from yufmusicgen_amd.synth import rosa_inputs
+
+    B, T, D = 8, 2048, 128
+    cand, write, read_raw, decay, u = [torch.from_numpy(x).cuda() for x in rosa_inputs(4, B, T, D)]
+    mem = torch.zeros(B, D, device="cuda")
+    out = torch.empty(B, T, D, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    run = lambda: check(lib().yuf_rosa_scan_f32(B, T, D, cand.data_ptr(), write.data_ptr(),  # noqa: E731
+                                                read_raw.data_ptr(), decay.data_ptr(), u.data_ptr(),
+                                                mem.data_ptr(), mem.data_ptr(), out.data_ptr(), st))
+    run()
+    torch.cuda.synchronize()
+    ms = time_events(run, iters, torch.cuda.current_stream())
+    nbytes = 4 * (4 * B * T * D + 2 * B * D)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "kernel": "rosa operator, segmented (rosa_power/scan/carry/final; C3 layer: B=8 T=2048 D=128)",
             "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
 
 
@@ -198,7 +253,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5"], default=None,
+    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5", "kernels"], default=None,
                     help="profiling aids: just the C2 scan (20 launches), just the prefill steps, just the C4 "
                          "decode leg, or a plain 256 MiB device copy (20 launches) that calibrates the "
                          "FETCH_SIZE/WRITE_SIZE counters")
@@ -212,6 +267,10 @@ def main() -> int:
 
     if args.only == "scan":
         print(json.dumps({"roofline": bench_scan(20)}), flush=True)
+        return 0
+    if args.only == "kernels":  # the three HBM-bound kernel legs, for one profiling run
+        print(json.dumps({"roofline": bench_scan(20), "decode_roofline": bench_wkv_step(50),
+                          "rosa_roofline": bench_rosa(20)}), flush=True)
         return 0
     if args.only == "copy":
         src = torch.ones(64 << 20, device="cuda")
@@ -300,6 +359,10 @@ def main() -> int:
     log("scan roofline")
     roofline = bench_scan(20)
     log(f"scan {roofline['avg_us']} us, {roofline['achieved']} GB/s")
+    step = bench_wkv_step(50)
+    log(f"wkv step {step['avg_us']} us, {step['achieved']} GB/s")
+    rosa = bench_rosa(20)
+    log(f"rosa {rosa['avg_us']} us, {rosa['achieved']} GB/s")
     gemm = bench_gemm(10)
     log(f"gemm {gemm['achieved']} TFLOP/s")
     cpu = None
@@ -330,6 +393,8 @@ def main() -> int:
         "decode_tokens_per_s": round(decode_tps, 1),
         "decode_ms_per_step": round(dec_elapsed * 1e3 / args.decode_steps, 3),
         "roofline": roofline,
+        "decode_roofline": step,
+        "rosa_roofline": rosa,
         "gemm_roofline": gemm,
         "cpu_baseline": cpu,
     }

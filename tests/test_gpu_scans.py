@@ -160,6 +160,28 @@ def test_rosa_full_size(decay_value):
     np.testing.assert_allclose(m.cpu().numpy(), me.numpy(), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("dim,steps,gated", [(64, 128, True), (128, 640, False), (256, 256, True), (128, 2048, True)])
+def test_rosa_segmented_operator(dim, steps, gated, monkeypatch):
+    """The operator's segmented form (T a multiple of 64, T >= 128, D in {64,
+    128, 256}: A^64 built on the device in double, segments from zero, the
+    carry chain, segments from their starts) against the float64 oracle and
+    against the sequential scan (YUF_ROSA_SEGMENTED=0), from a non-zero memory."""
+    from yufmusicgen_amd.ops import rosa_householder_scan
+
+    print(f"rosa segmented D={dim} T={steps} gated={gated}", flush=True)
+    cand, write, read_raw, decay, u = rosa_inputs(12 + dim, 3, steps, dim)
+    m0 = np.random.default_rng(6).standard_normal((3, dim)).astype(np.float32)
+    arrs = (cand, write, read_raw, decay, u, m0)
+    read, m = rosa_householder_scan(*(_dev(x) for x in arrs), gated=gated)
+    re, me = orosa.rosa_scan(*(torch.from_numpy(x.astype(np.float64)) for x in arrs), gated=gated)
+    np.testing.assert_allclose(read.cpu().numpy(), re.numpy(), rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(m.cpu().numpy(), me.numpy(), rtol=RTOL, atol=ATOL)
+    monkeypatch.setenv("YUF_ROSA_SEGMENTED", "0")
+    read_s, m_s = rosa_householder_scan(*(_dev(x) for x in arrs), gated=gated)
+    np.testing.assert_allclose(read.cpu().numpy(), read_s.cpu().numpy(), rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(m.cpu().numpy(), m_s.cpu().numpy(), rtol=RTOL, atol=ATOL)
+
+
 def test_rosa_chunked_continuation():
     """Scanning T tokens in ragged pieces, carrying the memory, equals one scan."""
     from yufmusicgen_amd.ops import rosa_householder_scan

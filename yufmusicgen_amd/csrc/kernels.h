@@ -55,6 +55,9 @@ hipError_t launch_rosa(const RosaParams &p, hipStream_t stream);
 // start, then true start) around a carry pass with AL = A^L ([D][D] row-major,
 // fp32).  Scratch: z, carry, ends of B * (T / L) * D floats each.
 bool rosa_segmented_ok(int T, int D, int L);
+// A^L of A = diag(lambda) (I - 2 u u^T) into AL [D][D] (column j = A^L e_j),
+// computed in double on the device (lambda post-sigmoid, u unit).
+hipError_t launch_rosa_power(int D, int L, const float *lambda, const float *u, float *AL, hipStream_t stream);
 hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry, float *ends,
                                  hipStream_t stream);
 

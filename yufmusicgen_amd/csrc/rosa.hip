@@ -32,6 +32,12 @@
 #include "common.h"
 #include "kernels.h"
 
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace yuf {
 namespace {
 
@@ -438,6 +444,45 @@ __global__ void rosa_final_kernel(int P, int D, const float *ends, const int *sl
         memory_out[(size_t)sl * D + c] = ends[((size_t)b * P + P - 1) * D + c];
 }
 
+// A^L of the ROSA transition A = diag(lambda) (I - 2 u u^T) for the operator
+// path (lambda post-sigmoid, u unit), in double precision like the engine's
+// host-side copy: wave w of workgroup g applies A L times to e_j, j = 4 g + w,
+// through the rank-one form A x = lambda (x - 2 (u.x) u); AL[i][j] = x_i.
+__global__ void __launch_bounds__(256) rosa_power_kernel(int D, int L, const float *lambda, const float *u, float *AL) {
+    const int j = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (j >= D) return;  // uniform over the wave
+    constexpr int kMaxPer = 16;  // D <= 1024
+    const int per = (D + 63) / 64;
+    double x[kMaxPer], uu[kMaxPer], lam[kMaxPer];
+#pragma unroll
+    for (int e = 0; e < kMaxPer; ++e) {
+        const int i = lane + 64 * e;
+        const bool in = e < per && i < D;
+        x[e] = in && i == j ? 1.0 : 0.0;
+        uu[e] = in ? (double)u[i] : 0.0;
+        lam[e] = in ? (double)lambda[i] : 0.0;
+    }
+    for (int step = 0; step < L; ++step) {
+        double pr = 0.0;
+#pragma unroll
+        for (int e = 0; e < kMaxPer; ++e) pr += uu[e] * x[e];
+        pr = wave_sum_f64(pr);
+#pragma unroll
+        for (int e = 0; e < kMaxPer; ++e) x[e] = lam[e] * (x[e] - 2.0 * pr * uu[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < kMaxPer; ++e) {
+        const int i = lane + 64 * e;
+        if (e < per && i < D) AL[(size_t)i * D + j] = (float)x[e];
+    }
+}
+
+hipError_t launch_rosa_power(int D, int L, const float *lambda, const float *u, float *AL, hipStream_t stream) {
+    if (D < 1 || D > 1024 || L < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rosa_power_kernel, dim3((D + 3) / 4), dim3(256), 0, stream, D, L, lambda, u, AL);
+    return hipGetLastError();
+}
+
 bool rosa_segmented_ok(int T, int D, int L) {
     return L > 0 && T % L == 0 && T / L >= 2 && (D == 64 || D == 128 || D == 256);
 }
@@ -467,6 +512,41 @@ hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, fl
         hipLaunchKernelGGL(rosa_final_kernel, dim3(p.B), dim3(256), 0, stream, P, p.D, ends, p.slot, p.memory_out);
     return hipGetLastError();
 }
+
+namespace {
+// Operator path: segment length of the segmented scan, and its scratch, one
+// growing buffer per (device, stream) kept for the life of the process (a
+// launch on a stream only ever waits on that stream's earlier work).
+constexpr int kOpRosaSeg = 64;
+std::mutex g_rosa_mu;
+std::map<std::pair<int, hipStream_t>, std::pair<float *, size_t>> g_rosa_scratch;
+
+bool op_rosa_sequential() {
+    const char *e = std::getenv("YUF_ROSA_SEGMENTED");
+    return e && std::strcmp(e, "0") == 0;
+}
+
+hipError_t op_rosa_scratch(hipStream_t stream, size_t floats, float **out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return err;
+    std::lock_guard<std::mutex> lock(g_rosa_mu);
+    auto &slot = g_rosa_scratch[{dev, stream}];
+    if (slot.second < floats) {
+        if (slot.first) {
+            // Earlier launches on this stream may still read the old buffer.
+            if ((err = hipStreamSynchronize(stream)) != hipSuccess) return err;
+            (void)hipFree(slot.first);
+            slot = {nullptr, 0};
+        }
+        float *p = nullptr;
+        if ((err = hipMalloc(&p, floats * sizeof(float))) != hipSuccess) return err;
+        slot = {p, floats};
+    }
+    *out = slot.first;
+    return hipSuccess;
+}
+}  // namespace
 
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
     if (p.B <= 0) return hipSuccess;
@@ -507,7 +587,21 @@ extern "C" int yuf_rosa_scan_f32(int B, int T, int D, const float *cand, const f
     p.cand = cand; p.write = write; p.read_raw = read_raw;
     p.decay = decay; p.direction = direction;
     p.memory_in = memory_in; p.memory_out = memory_out; p.read_out = read_out;
-    hipError_t err = launch_rosa(p, static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t err;
+    if (B > 0 && rosa_segmented_ok(T, D, kOpRosaSeg) && !op_rosa_sequential()) {
+        // Segmented form (as the engine's prefill): A^L on the device, then
+        // segments from zero, the carry chain, and segments from their starts.
+        float *scratch = nullptr;
+        const size_t seg = (size_t)B * (T / kOpRosaSeg) * D;
+        if ((err = op_rosa_scratch(st, (size_t)D * D + 3 * seg, &scratch)) != hipSuccess)
+            return fail(YUF_ERR_OOM, std::string("rosa scratch: ") + hipGetErrorString(err));
+        float *AL = scratch, *z = AL + (size_t)D * D, *carry = z + seg, *ends = carry + seg;
+        err = launch_rosa_power(D, kOpRosaSeg, decay, direction, AL, st);
+        if (err == hipSuccess) err = launch_rosa_segmented(p, AL, kOpRosaSeg, z, carry, ends, st);
+    } else {
+        err = launch_rosa(p, st);
+    }
     if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("rosa launch: ") + hipGetErrorString(err));
     return YUF_OK;
 }
