@@ -306,105 +306,138 @@ __global__ void __launch_bounds__(kWave) wkv7_scan_kernel(WkvParams p, int waves
     }
 }
 
-// Single-token step (T = 1, decode): the same lane layout as the scan (L lanes
-// per state row, E columns per lane, R rows per wave), but with no LDS staging:
-// every lane loads its E columns of r, w, k, a (b), k_k, k_a and its rows' v
-// and state straight from global memory, all issued before the first use, so a
-// step costs one memory round trip.  The per-head L2 norm of k * k_k is an
-// L-lane butterfly (each row's L lanes cover all N columns), as are S a and
-// S r.  Four waves per workgroup, B * H * W waves in all.
+// Single-token step (T = 1, decode): one 256-thread workgroup per (stream,
+// head).  The state streams in and out as 16-byte runs (float4 q of the
+// row-major N x N state is row 4q / N, columns 4q % N .. + 3; N % 4 == 0); the
+// per-token vectors are prepared once per head in LDS (decay, and in the model
+// path kappa = normalize(k k_k), a = -kappa, b = kappa alpha, k^ = k (1 +
+// (alpha - 1) k_a)); the row sums S a and S' r go through per-float4 partials
+// in LDS.  Every global load is issued before the first barrier, so a step
+// costs one HBM round trip plus four barriers.
+constexpr int kStepThreads = 256;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 template <int N, bool PREP>
-__global__ void __launch_bounds__(256) wkv7_step_kernel(WkvParams p, int waves_total) {
-    using Lay = Layout<N>;
-    constexpr int E = Lay::E, L = Lay::L, R = Lay::R, W = Lay::W;
-    const int flat = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (flat >= waves_total) return;
-    const int lane = threadIdx.x & 63;
-    const int head = flat / W, wave = flat - head * W;
+__global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
+    constexpr int Q = N * N / 4;                                 // float4 of the state
+    constexpr int QM = (Q + kStepThreads - 1) / kStepThreads;   // per thread
+    constexpr int RQ = N / 4;                                    // float4 per row
+    __shared__ __attribute__((aligned(16))) float vec[6][N];     // a, b, k^, d, r, v
+    __shared__ float part[Q];                                    // per-float4 partial row sums
+    __shared__ float rowv[N];                                    // S a, then y
+    __shared__ float red[kStepThreads / 64];
+
+    const int head = blockIdx.x;
     const int bb = head / p.H, h = head - bb * p.H;
-    const int rl = lane / L, cl = lane - rl * L;
-    const int i = wave * R + rl, j0 = cl * E;
-    const bool row_ok = i < N;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int slot = p.slot ? p.slot[bb] : bb;
     const size_t state_off = ((size_t)slot * p.H + h) * N * N;
     const size_t base = ((size_t)bb * p.H + h) * N;  // token (bb, 0)
 
+    // All global loads first: the state's float4s, then one column / row per thread.
     const auto rs = make_rsrc(p.state_in ? p.state_in + state_off : nullptr, p.state_in ? N * N * 4 : 0u);
-    const auto rr = make_rsrc(p.r + base, N * 4), rw = make_rsrc(p.w + base, N * 4);
-    const auto rk = make_rsrc(p.k + base, N * 4), ra = make_rsrc(p.a + base, N * 4);
-    const auto rb = make_rsrc(PREP ? nullptr : p.b + base, PREP ? 0u : N * 4);
-    const auto rkk = make_rsrc(PREP ? p.k_k + h * N : nullptr, PREP ? N * 4 : 0u);
-    const auto rka = make_rsrc(PREP ? p.k_a + h * N : nullptr, PREP ? N * 4 : 0u);
-    float s[E], rv[E], wv[E], kv[E], av[E], bv[E], kk[E], ka[E];
+    float4 sq[QM];
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-        const uint32_t off = (uint32_t)(j0 + e) * 4u;
-        s[e] = buf_load(rs, row_ok ? (uint32_t)(i * N + j0 + e) * 4u : kBufferOob);
-        rv[e] = buf_load(rr, off);
-        wv[e] = buf_load(rw, off);
-        kv[e] = buf_load(rk, off);
-        av[e] = buf_load(ra, off);
-        if constexpr (PREP) {
-            kk[e] = buf_load(rkk, off);
-            ka[e] = buf_load(rka, off);
-        } else {
-            bv[e] = buf_load(rb, off);
-        }
+    for (int m = 0; m < QM; ++m) {
+        const int q = tid + m * kStepThreads;
+        sq[m] = buf_load4(rs, q < Q ? (uint32_t)q * 16u : kBufferOob);
     }
-    const float vi = buf_load(make_rsrc(p.v + base, N * 4), row_ok ? (uint32_t)i * 4u : kBufferOob);
-
-    float dv[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        // d = exp(-e^{-0.5} sigmoid(w)) = exp2(-e^{-0.5} log2(e) sigmoid(w)).
-        const float sig = __frcp_rn(1.0f + __expf(-wv[e]));
-        dv[e] = exp2f(-0.8750387749f * sig);
+    const bool col = tid < N;
+    const uint32_t off = col ? (uint32_t)tid * 4u : kBufferOob;
+    const float rv = buf_load(make_rsrc(p.r + base, N * 4), off);
+    const float wv = buf_load(make_rsrc(p.w + base, N * 4), off);
+    float kv = buf_load(make_rsrc(p.k + base, N * 4), off);
+    float av = buf_load(make_rsrc(p.a + base, N * 4), off);
+    const float vv = buf_load(make_rsrc(p.v + base, N * 4), off);
+    float bv = 0.0f, kk = 0.0f, ka = 0.0f;
+    if constexpr (PREP) {
+        kk = buf_load(make_rsrc(p.k_k + h * N, N * 4), off);
+        ka = buf_load(make_rsrc(p.k_a + h * N, N * 4), off);
+    } else {
+        bv = buf_load(make_rsrc(p.b + base, N * 4), off);
     }
     if constexpr (PREP) {
         // kappa = normalize(k * k_k) over the head (F.normalize, eps 1e-12).
-        float sq = 0.0f;
+        const float x = kv * kk;
+        const float ws = wave_sum(x * x);
+        if (lane == 0) red[wave] = ws;
+        lds_barrier();
+        float sq2 = 0.0f;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const float x = kv[e] * kk[e];
-            sq = fmaf(x, x, sq);
-        }
-        const float inv = 1.0f / fmaxf(sqrtf(group_sum<L>(sq)), 1e-12f);
+        for (int w = 0; w < (N + 63) / 64; ++w) sq2 += red[w];
+        const float inv = 1.0f / fmaxf(sqrtf(sq2), 1e-12f);
+        const float kap = x * inv, alpha = av;
+        av = -kap;
+        bv = kap * alpha;
+        kv = kv * (1.0f + (alpha - 1.0f) * ka);
+    }
+    if (col) {
+        // d = exp(-e^{-0.5} sigmoid(w)) = exp2(-e^{-0.5} log2(e) sigmoid(w)).
+        const float sig = __frcp_rn(1.0f + __expf(-wv));
+        vec[0][tid] = av;
+        vec[1][tid] = bv;
+        vec[2][tid] = kv;
+        vec[3][tid] = exp2f(-0.8750387749f * sig);
+        vec[4][tid] = rv;
+        vec[5][tid] = vv;
+    }
+    lds_barrier();
+    // sa_i = sum_j S_ij a_j.
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-            const float kap = kv[e] * kk[e] * inv;
-            const float alpha = av[e];
-            av[e] = -kap;
-            bv[e] = kap * alpha;
-            kv[e] = kv[e] * (1.0f + (alpha - 1.0f) * ka[e]);
+    for (int m = 0; m < QM; ++m) {
+        const int q = tid + m * kStepThreads;
+        if (q < Q) {
+            const float4 a4 = *reinterpret_cast<const float4 *>(&vec[0][(4 * q) % N]);
+            part[q] = (sq[m].x * a4.x + sq[m].y * a4.y) + (sq[m].z * a4.z + sq[m].w * a4.w);
         }
     }
-    float sa = 0.0f;
+    lds_barrier();
+    if (tid < N) {
+        float sa = 0.0f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) sa = fmaf(s[e], av[e], sa);
-    sa = group_sum<L>(sa);
-    float yv = 0.0f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-        s[e] = fmaf(s[e], dv[e], fmaf(sa, bv[e], kv[e] * vi));
-        yv = fmaf(s[e], rv[e], yv);
+        for (int u = 0; u < RQ; ++u) sa += part[tid * RQ + u];
+        rowv[tid] = sa;
     }
-    yv = group_sum<L>(yv);
-    if (row_ok && cl == 0) p.y[base + i] = yv;
-    if (p.state_out && row_ok) {
+    lds_barrier();
+    // S'_ij = S_ij d_j + sa_i b_j + v_i k^_j;  y_i = sum_j S'_ij r_j.
+    const auto ro = make_rsrc(p.state_out ? p.state_out + state_off : nullptr, p.state_out ? N * N * 4 : 0u);
 #pragma unroll
-        for (int e = 0; e < E; ++e) p.state_out[state_off + (size_t)i * N + j0 + e] = s[e];
+    for (int m = 0; m < QM; ++m) {
+        const int q = tid + m * kStepThreads;
+        if (q < Q) {
+            const int i = (4 * q) / N, c = (4 * q) % N;
+            const float sa = rowv[i], vi = vec[5][i];
+            const float4 b4 = *reinterpret_cast<const float4 *>(&vec[1][c]);
+            const float4 k4 = *reinterpret_cast<const float4 *>(&vec[2][c]);
+            const float4 d4 = *reinterpret_cast<const float4 *>(&vec[3][c]);
+            const float4 r4 = *reinterpret_cast<const float4 *>(&vec[4][c]);
+            float4 x;
+            x.x = fmaf(sq[m].x, d4.x, fmaf(sa, b4.x, k4.x * vi));
+            x.y = fmaf(sq[m].y, d4.y, fmaf(sa, b4.y, k4.y * vi));
+            x.z = fmaf(sq[m].z, d4.z, fmaf(sa, b4.z, k4.z * vi));
+            x.w = fmaf(sq[m].w, d4.w, fmaf(sa, b4.w, k4.w * vi));
+            part[q] = (x.x * r4.x + x.y * r4.y) + (x.z * r4.z + x.w * r4.w);
+            if (p.state_out)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, (uint32_t)q * 16u, 0, 0);
+        }
+    }
+    lds_barrier();
+    if (tid < N) {
+        float yv = 0.0f;
+#pragma unroll
+        for (int u = 0; u < RQ; ++u) yv += part[tid * RQ + u];
+        p.y[base + tid] = yv;
     }
 }
 
 template <int N>
 hipError_t launch_step_n(const WkvParams &p, bool prep, hipStream_t stream) {
-    using Lay = Layout<N>;
-    const int waves = p.B * p.H * Lay::W;
-    const dim3 grid((waves + 3) / 4), block(256);
+    static_assert(N % 4 == 0 && N <= kStepThreads, "step kernel layout");
+    const dim3 grid(p.B * p.H), block(kStepThreads);
     if (prep)
-        hipLaunchKernelGGL((wkv7_step_kernel<N, true>), grid, block, 0, stream, p, waves);
+        hipLaunchKernelGGL((wkv7_step_kernel<N, true>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((wkv7_step_kernel<N, false>), grid, block, 0, stream, p, waves);
+        hipLaunchKernelGGL((wkv7_step_kernel<N, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 
