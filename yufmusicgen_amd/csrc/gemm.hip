@@ -549,6 +549,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
 constexpr int kDecWaves = 8, kDecThreads = kDecWaves * 64;
 constexpr int kMaxDecode = kMaxGroup;
 constexpr int kDecLnPerLane = 16;  // LayerNorm prologue: K <= 1024
+static_assert(64 * kDecLnPerLane <= 2 * kDecThreads, "gamma / beta: at most two columns per thread");
 
 struct DecodeGroup {
     GemmParams p[kMaxDecode];
@@ -558,7 +559,7 @@ struct DecodeGroup {
 };
 
 // Largest S (k steps in flight per wave) that keeps the prefetched operands
-// within the register budget of a 1024-thread workgroup (128 VGPRs per lane).
+// within the register budget of a 512-thread workgroup.
 // A WB step covers 32 k and holds 8 A floats per m-tile (4 for fp32 W).
 constexpr int dec_cap(int NT, int MI, int PRO, bool WB = false) {
     const int c = MI == 1 ? (NT == 1 && PRO < 2 ? 10 : 6) : (NT == 1 ? (PRO == 0 ? 4 : 3) : 3);
@@ -613,40 +614,78 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
     auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
-    auto load_round = [&](int k0) {
-        const auto rt = make_rsrc(PRO == 2 ? p.a_gate + (size_t)row0 * p.ldg : nullptr,
-                                  PRO == 2 ? (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4) : 0u);
+    const auto rt = make_rsrc(PRO == 2 ? p.a_gate + (size_t)row0 * p.ldg : nullptr,
+                              PRO == 2 ? (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4) : 0u);
+    auto load_w = [&](int s, int k0) {
+        const int k = k0 + KS * s + RL * g4;
+        const bool kin = k < k_end;  // K % RL == 0 on this path
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int k = k0 + KS * s + RL * g4;
-            const bool kin = k < k_end;  // K % RL == 0 on this path
+        for (int t = 0; t < NT; ++t) {
+            const int wr = w_row0 + 32 * t + li;
+            b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * (WB ? 2u : 4u) : kBufferOob);
+        }
+    };
+    auto load_a = [&](int s, int k0) {
+        const int k = k0 + KS * s + RL * g4;
+        const bool kin = k < k_end;
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const int wr = w_row0 + 32 * t + li;
-                b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * (WB ? 2u : 4u) : kBufferOob);
-            }
+        for (int i = 0; i < MI; ++i)
+#pragma unroll
+            for (int hh = 0; hh < AH; ++hh)
+                a[s][i][hh] = load4(ra, kin ? (uint32_t)((size_t)(16 * i + li) * p.lda + k + 4 * hh) * 4u : kBufferOob);
+        if constexpr (PRO == 2) {
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int hh = 0; hh < AH; ++hh)
-                    a[s][i][hh] = load4(ra, kin ? (uint32_t)((size_t)(16 * i + li) * p.lda + k + 4 * hh) * 4u : kBufferOob);
-            if constexpr (PRO == 2) {
+                    gt[s][i][hh] = load4(rt, kin ? (uint32_t)((size_t)(16 * i + li) * p.ldg + k + 4 * hh) * 4u : kBufferOob);
+        }
+    };
+    // Issue order: with a prologue, all A (and gate) loads of the round first,
+    // so the row statistics wait for A only while W is still in flight.
+    auto load_round = [&](int k0) {
+        if constexpr (PRO > 0) {
 #pragma unroll
-                for (int i = 0; i < MI; ++i)
+            for (int s = 0; s < S; ++s) load_a(s, k0);
 #pragma unroll
-                    for (int hh = 0; hh < AH; ++hh)
-                        gt[s][i][hh] = load4(rt, kin ? (uint32_t)((size_t)(16 * i + li) * p.ldg + k + 4 * hh) * 4u : kBufferOob);
+            for (int s = 0; s < S; ++s) load_w(s, k0);
+        } else {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                load_w(s, k0);
+                load_a(s, k0);
             }
         }
     };
-    load_round(k_begin);
+    // gamma and beta of the K columns (K <= 2 * kDecThreads), loaded between
+    // the round's A and W loads.
+    float gam[2], bet[2];
+    if constexpr (PRO > 0) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) load_a(s, k_begin);
+        const auto rg = make_rsrc(p.ln_gamma, (uint32_t)p.K * 4u), rb = make_rsrc(p.ln_beta, (uint32_t)p.K * 4u);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = tid + j * kDecThreads;
+            gam[j] = buf_load(rg, c < p.K ? (uint32_t)c * 4u : kBufferOob);
+            bet[j] = buf_load(rb, c < p.K ? (uint32_t)c * 4u : kBufferOob);
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) load_w(s, k_begin);
+    } else {
+        load_round(k_begin);
+    }
 
     float mean[MI], rstd[MI];
     if constexpr (PRO > 0) {
         // gamma and beta of the K columns, shared by every row of the tile.
-        for (int c = tid; c < p.K; c += kDecThreads) {
-            affine[c] = p.ln_gamma[c];
-            affine[64 * kDecLnPerLane + c] = p.ln_beta[c];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int c = tid + j * kDecThreads;
+            if (c < p.K) {
+                affine[c] = gam[j];
+                affine[64 * kDecLnPerLane + c] = bet[j];
+            }
         }
         if (spw <= S) {
             // One round covers this wave's K range, so the row statistics come
@@ -990,6 +1029,7 @@ void launch_dec(const DecodeGroup &g, int S, dim3 grid, hipStream_t stream) {
         case 2: launch_dec_s<NT, MI, PRO, WB, 2>(g, grid, stream); break;
         case 3: launch_dec_s<NT, MI, PRO, WB, 3>(g, grid, stream); break;
         case 4: launch_dec_s<NT, MI, PRO, WB, 4>(g, grid, stream); break;
+        case 5: launch_dec_s<NT, MI, PRO, WB, 5>(g, grid, stream); break;
         case 6: launch_dec_s<NT, MI, PRO, WB, 6>(g, grid, stream); break;
         default: launch_dec_s<NT, MI, PRO, WB, 10>(g, grid, stream); break;
     }
@@ -1017,7 +1057,7 @@ void launch_dec_kind(const DecodeGroup &g, int NT, int MI, int PRO, int S, dim3 
 // Smallest instantiated S >= min(steps per wave, cap).
 int pick_steps(int spw, int cap) {
     const int want = std::min(spw, cap);
-    for (int s : {1, 2, 3, 4, 6, 10})
+    for (int s : {1, 2, 3, 4, 5, 6, 10})
         if (s >= want && s <= cap) return s;
     return cap;
 }
@@ -1039,14 +1079,18 @@ hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
         }
         return hipSuccess;
     }
-    int units1 = 0, spw = 1;
+    int units1 = 0, spw = 1, mrows = 0;
     for (int i = 0; i < count; ++i) {
         const GemmParams &p = ps[i];
         const int slices = p.silu_pair ? p.N / 32 : (p.N + 15) / 16;
         units1 += slices * ((p.M + 15) / 16);
         spw = std::max(spw, ((p.K + KS - 1) / KS + kDecWaves - 1) / kDecWaves);
+        mrows = std::max(mrows, p.M);
     }
     // Wide products (the LM head) already fill the chip with 64-row tiles.
+    // (Measured: the LN + SiLU-pair FFN input is slower with them, 17.7 against
+    // 15.1 us at 64 x 5120 x 640, so it keeps 16-row tiles.)
+    (void)mrows;
     const int MI = (units1 > 1024 && PRO < 2 && !(PRO == 1 && NT == 2)) ? 4 : 1;
     DecodeGroup g{};
     g.count = count;
