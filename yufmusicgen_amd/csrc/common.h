@@ -72,6 +72,35 @@ __device__ __forceinline__ float wave_sum(float x) {
     return (s0 + s1) + (s2 + s3);
 }
 
+// Full 64-lane sum of a double, returned to every lane with the same bits:
+// DPP inside each 16-lane row (each step adds a pair of partial sums that both
+// lanes of the pair see, so commutativity keeps them equal), then the gfx950
+// row swaps pair rows (0,1) (2,3) and then (0,2) (1,3).  No LDS traffic.
+template <int CTRL>
+__device__ __forceinline__ double dpp_move_f64(double x) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, CTRL, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    x += dpp_move_f64<dpp::kQuadXor1>(x);
+    x += dpp_move_f64<dpp::kQuadXor2>(x);
+    x += dpp_move_f64<dpp::kRowHalfMirror>(x);
+    x += dpp_move_f64<dpp::kRowMirror>(x);
+    uint64_t b = __builtin_bit_cast(uint64_t, x);
+    const auto l16 = __builtin_amdgcn_permlane16_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto h16 = __builtin_amdgcn_permlane16_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    x = __builtin_bit_cast(double, ((uint64_t)h16[0] << 32) | l16[0]) +
+        __builtin_bit_cast(double, ((uint64_t)h16[1] << 32) | l16[1]);
+    b = __builtin_bit_cast(uint64_t, x);
+    const auto l32 = __builtin_amdgcn_permlane32_swap((uint32_t)b, (uint32_t)b, false, false);
+    const auto h32 = __builtin_amdgcn_permlane32_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
+    return __builtin_bit_cast(double, ((uint64_t)h32[0] << 32) | l32[0]) +
+           __builtin_bit_cast(double, ((uint64_t)h32[1] << 32) | l32[1]);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also releases

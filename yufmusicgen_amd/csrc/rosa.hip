@@ -327,13 +327,6 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
 
 }  // namespace
 
-__device__ __forceinline__ double wave_sum_f64(double x) {
-    // xor butterfly: both lanes of every pair add the same two values, so all
-    // lanes end with the same bits.
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-}
 
 // Single-token step (T = 1, decode): one wave per stream, EPL channels per
 // lane, the direct recurrence with its two projections (u.m_{t-1} and u.m_t)
@@ -422,18 +415,20 @@ __global__ void __launch_bounds__(1024) rosa_carry_kernel(int P, int D, const fl
     for (int j = 0; j < 64; ++j) arow[j] = AL[(size_t)r * D + q * 64 + j];
     const int sl = slot ? slot[b] : b;
     if (tid < D) st[tid] = memory_in ? memory_in[(size_t)sl * D + tid] : 0.0f;
-    __syncthreads();
+    // LDS-only barriers: the carry stores below stay in flight across them.
+    lds_barrier();
     for (int s = 0; s < P; ++s) {
         const size_t v = (size_t)b * P + s;
         if (tid < D) carry[v * D + tid] = st[tid];
+        const float zr = q == 0 ? z[v * D + r] : 0.0f;
         float dot = 0.0f;
 #pragma unroll
         for (int j = 0; j < 64; ++j) dot = fmaf(arow[j], st[q * 64 + j], dot);
         // the tpr partial dot products of a row sit in adjacent lanes
         for (int o = 1; o < tpr; o <<= 1) dot += __shfl_xor(dot, o);
-        __syncthreads();
-        if (q == 0) st[r] = dot + z[v * D + r];
-        __syncthreads();
+        lds_barrier();
+        if (q == 0) st[r] = dot + zr;
+        lds_barrier();
     }
 }
 
@@ -448,16 +443,17 @@ __global__ void rosa_final_kernel(int P, int D, const float *ends, const int *sl
 // path (lambda post-sigmoid, u unit), in double precision like the engine's
 // host-side copy: wave w of workgroup g applies A L times to e_j, j = 4 g + w,
 // through the rank-one form A x = lambda (x - 2 (u.x) u); AL[i][j] = x_i.
+// PER = ceil(D / 64) rows per lane; the L projections u.x are the chain, each
+// one DPP / row-swap reduction.
+template <int PER>
 __global__ void __launch_bounds__(256) rosa_power_kernel(int D, int L, const float *lambda, const float *u, float *AL) {
     const int j = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (j >= D) return;  // uniform over the wave
-    constexpr int kMaxPer = 16;  // D <= 1024
-    const int per = (D + 63) / 64;
-    double x[kMaxPer], uu[kMaxPer], lam[kMaxPer];
+    double x[PER], uu[PER], lam[PER];
 #pragma unroll
-    for (int e = 0; e < kMaxPer; ++e) {
+    for (int e = 0; e < PER; ++e) {
         const int i = lane + 64 * e;
-        const bool in = e < per && i < D;
+        const bool in = i < D;
         x[e] = in && i == j ? 1.0 : 0.0;
         uu[e] = in ? (double)u[i] : 0.0;
         lam[e] = in ? (double)lambda[i] : 0.0;
@@ -465,21 +461,27 @@ __global__ void __launch_bounds__(256) rosa_power_kernel(int D, int L, const flo
     for (int step = 0; step < L; ++step) {
         double pr = 0.0;
 #pragma unroll
-        for (int e = 0; e < kMaxPer; ++e) pr += uu[e] * x[e];
+        for (int e = 0; e < PER; ++e) pr += uu[e] * x[e];
         pr = wave_sum_f64(pr);
 #pragma unroll
-        for (int e = 0; e < kMaxPer; ++e) x[e] = lam[e] * (x[e] - 2.0 * pr * uu[e]);
+        for (int e = 0; e < PER; ++e) x[e] = lam[e] * (x[e] - 2.0 * pr * uu[e]);
     }
 #pragma unroll
-    for (int e = 0; e < kMaxPer; ++e) {
+    for (int e = 0; e < PER; ++e) {
         const int i = lane + 64 * e;
-        if (e < per && i < D) AL[(size_t)i * D + j] = (float)x[e];
+        if (i < D) AL[(size_t)i * D + j] = (float)x[e];
     }
 }
 
 hipError_t launch_rosa_power(int D, int L, const float *lambda, const float *u, float *AL, hipStream_t stream) {
     if (D < 1 || D > 1024 || L < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(rosa_power_kernel, dim3((D + 3) / 4), dim3(256), 0, stream, D, L, lambda, u, AL);
+    const dim3 grid((D + 3) / 4), block(256);
+    const int per = (D + 63) / 64;
+    if (per <= 1) hipLaunchKernelGGL(rosa_power_kernel<1>, grid, block, 0, stream, D, L, lambda, u, AL);
+    else if (per <= 2) hipLaunchKernelGGL(rosa_power_kernel<2>, grid, block, 0, stream, D, L, lambda, u, AL);
+    else if (per <= 4) hipLaunchKernelGGL(rosa_power_kernel<4>, grid, block, 0, stream, D, L, lambda, u, AL);
+    else if (per <= 8) hipLaunchKernelGGL(rosa_power_kernel<8>, grid, block, 0, stream, D, L, lambda, u, AL);
+    else hipLaunchKernelGGL(rosa_power_kernel<16>, grid, block, 0, stream, D, L, lambda, u, AL);
     return hipGetLastError();
 }
 
