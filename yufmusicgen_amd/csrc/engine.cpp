@@ -393,6 +393,8 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         const float *mr = a.mix, *mw = a.mix + plane, *mk = a.mix + 2 * plane, *mv = a.mix + 3 * plane,
                     *ma = a.mix + 4 * plane, *mg = a.mix + 5 * plane;
         int rc;
+        // Decode with fp32 weights: the second low-rank stage runs inside the WKV step.
+        const bool fuse_lr = Tc == 1 && !e.w_h && wkv7_step_lowrank_ok(s.head_size, L);
         {
             // r, k, v and the three low-rank first stages (one launch for short
             // products, two otherwise: the tile widths differ); then the second stages.
@@ -409,16 +411,23 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
                 if ((rc = gemm_group(st, g6, 3)) != YUF_OK) return rc;
                 if ((rc = gemm_group(st, g6 + 3, 3)) != YUF_OK) return rc;
             }
-            GemmParams l2[3] = {make_gemm(e, M, d, L, lw, L, w.w2t, L, a.wr, d, w.w0),
-                                make_gemm(e, M, d, L, la, L, w.a2t, L, a.al, d, w.a0, ACT_SIGMOID),
-                                make_gemm(e, M, d, L, lg, L, w.g2t, L, a.g, d, nullptr, ACT_SIGMOID)};
-            if ((rc = gemm_group(st, l2, 3)) != YUF_OK) return rc;
+            if (!fuse_lr) {
+                GemmParams l2[3] = {make_gemm(e, M, d, L, lw, L, w.w2t, L, a.wr, d, w.w0),
+                                    make_gemm(e, M, d, L, la, L, w.a2t, L, a.al, d, w.a0, ACT_SIGMOID),
+                                    make_gemm(e, M, d, L, lg, L, w.g2t, L, a.g, d, nullptr, ACT_SIGMOID)};
+                if ((rc = gemm_group(st, l2, 3)) != YUF_OK) return rc;
+            }
         }
         WkvParams wp;
         wp.B = n; wp.T = Tc; wp.H = s.heads;
         wp.r = a.r; wp.w = a.wr; wp.k = a.k; wp.v = a.v; wp.a = a.al;
         wp.k_k = w.k_k; wp.k_a = w.k_a;
         wp.state_in = wkv; wp.state_out = wkv; wp.slot = a.slots; wp.y = a.y;
+        if (fuse_lr) {
+            // The step kernel computes w, alpha and g from the rank-L rows.
+            wp.lr = a.lr; wp.lr_plane = lplane; wp.L = L;
+            wp.w2t = w.w2t; wp.a2t = w.a2t; wp.g2t = w.g2t; wp.w0 = w.w0; wp.a0 = w.a0; wp.g_out = a.g;
+        }
         ENG_TRY(launch_wkv7(wp, s.head_size, true, st), "wkv7");
         if ((rc = ln_gemm(e, st, M, d, d, a.y, d, w.ln_o_w, w.ln_o_b, a.g, a.z, w.w_o, a.h, d, nullptr, a.h, d)) !=
             YUF_OK)

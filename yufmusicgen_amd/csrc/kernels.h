@@ -22,8 +22,21 @@ struct WkvParams {
     float *state_out = nullptr;
     const int *slot = nullptr;
     float *y = nullptr;  // [B, T, H, N]
+    // Decode step (T = 1, fused prep) with the second low-rank stage folded in:
+    // when `lr` is set, `w` and `a` are not read; instead, per channel c,
+    //   w = w0 + lw . w2t[c],  alpha = sigmoid(a0 + la . a2t[c]),
+    //   g = sigmoid(lg . g2t[c])  (written to g_out [B, H * N]),
+    // from the rank-L rows lw = lr + b * L, la = lw + lr_plane, lg = la + lr_plane
+    // and the [H * N, L] matrices w2t, a2t, g2t (yufmusicgen/model.py:108-112).
+    const float *lr = nullptr;
+    size_t lr_plane = 0;
+    int L = 0;
+    const float *w2t = nullptr, *a2t = nullptr, *g2t = nullptr, *w0 = nullptr, *a0 = nullptr;
+    float *g_out = nullptr;
 };
 bool wkv7_supported(int N);
+// The fused low-rank step exists for N <= 64 and L <= 128 with L % 8 == 0.
+bool wkv7_step_lowrank_ok(int N, int L);
 // Picks the chunked MFMA kernel (N <= 64, N % 4 == 0, T >= kWkvChunkMinT) or
 // the per-token VALU kernel; YUF_WKV7_KERNEL=serial|chunked forces one.
 hipError_t launch_wkv7(const WkvParams &p, int N, bool prep, hipStream_t stream);

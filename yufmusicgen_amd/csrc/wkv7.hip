@@ -306,36 +306,50 @@ __global__ void __launch_bounds__(kWave) wkv7_scan_kernel(WkvParams p, int waves
     }
 }
 
-// Single-token step (T = 1, decode): one 256-thread workgroup per (stream,
-// head).  The state streams in and out as 16-byte runs (float4 q of the
-// row-major N x N state is row 4q / N, columns 4q % N .. + 3; N % 4 == 0); the
-// per-token vectors are prepared once per head in LDS (decay, and in the model
-// path kappa = normalize(k k_k), a = -kappa, b = kappa alpha, k^ = k (1 +
-// (alpha - 1) k_a)); the row sums S a and S' r go through per-float4 partials
-// in LDS.  Every global load is issued before the first barrier, so a step
-// costs one HBM round trip plus four barriers.
+// Single-token step (T = 1, decode): 256 threads per (stream, head), SPW
+// streams of one head per workgroup.  The state streams in and out as 16-byte
+// runs (float4 q of the row-major N x N state is row 4q / N, columns 4q % N ..
+// + 3; N % 4 == 0); the per-token vectors are prepared once per head in LDS
+// (decay, and in the model path kappa = normalize(k k_k), a = -kappa, b = kappa
+// alpha, k^ = k (1 + (alpha - 1) k_a)); the row sums S a and S' r go through
+// per-float4 partials in LDS.  Every global load is issued before the first
+// barrier, so a step costs one HBM round trip plus four barriers.
+//
+// LR (model decode path): the second low-rank stage runs here instead of as a
+// GEMM -- w, alpha and the output gate g of the head's N channels are dot
+// products of the stream's rank-L rows with the head's N x L slices of w2t,
+// a2t, g2t, staged once per workgroup in LDS and shared by its SPW streams.
 constexpr int kStepThreads = 256;
+constexpr int kStepLrSpw = 4;       // streams per workgroup of the LR form
+constexpr int kStepLrMaxL = 128;  // an LDS weight row holds kStepLrMaxL + 2 floats (even / odd lanes on distinct banks)
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <int N, bool PREP>
-__global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
+template <int N, bool PREP, int SPW, bool LR>
+__global__ void __launch_bounds__(kStepThreads * SPW) wkv7_step_kernel(WkvParams p) {
+    static_assert(!LR || (PREP && 3 * N <= kStepThreads), "fused low-rank layout");
     constexpr int Q = N * N / 4;                                 // float4 of the state
     constexpr int QM = (Q + kStepThreads - 1) / kStepThreads;   // per thread
     constexpr int RQ = N / 4;                                    // float4 per row
-    __shared__ __attribute__((aligned(16))) float vec[6][N];     // a, b, k^, d, r, v
-    __shared__ float part[Q];                                    // per-float4 partial row sums
-    __shared__ float rowv[N];                                    // S a, then y
-    __shared__ float red[kStepThreads / 64];
+    constexpr int LP = kStepLrMaxL + 2;                          // padded LDS row of a weight slice
+    __shared__ __attribute__((aligned(16))) float vec[SPW][6][N];  // a, b, k^, d, r, v
+    __shared__ float part[SPW][Q];                                 // per-float4 partial row sums
+    __shared__ float rowv[SPW][N];                                 // S a, then y
+    __shared__ float red[SPW][kStepThreads / 64];
+    __shared__ float wl[LR ? 3 * N : 1][LR ? LP : 1];              // w2t | a2t | g2t rows of the head
+    __shared__ float lrs[LR ? SPW : 1][LR ? 3 : 1][LR ? kStepLrMaxL : 1];
+    __shared__ float lrv[LR ? SPW : 1][2][LR ? N : 1];             // w, alpha
 
-    const int head = blockIdx.x;
-    const int bb = head / p.H, h = head - bb * p.H;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int slot = p.slot ? p.slot[bb] : bb;
+    const int sub = threadIdx.x / kStepThreads, tid = threadIdx.x % kStepThreads;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x % p.H, bb = (blockIdx.x / p.H) * SPW + sub;
+    const bool live = bb < p.B;  // idle streams of the last workgroup still meet every barrier
+    const int slot = live ? (p.slot ? p.slot[bb] : bb) : 0;
     const size_t state_off = ((size_t)slot * p.H + h) * N * N;
-    const size_t base = ((size_t)bb * p.H + h) * N;  // token (bb, 0)
+    const size_t base = ((size_t)(live ? bb : 0) * p.H + h) * N;  // token (bb, 0)
 
     // All global loads first: the state's float4s, then one column / row per thread.
-    const auto rs = make_rsrc(p.state_in ? p.state_in + state_off : nullptr, p.state_in ? N * N * 4 : 0u);
+    const auto rs = make_rsrc(live && p.state_in ? p.state_in + state_off : nullptr,
+                              live && p.state_in ? N * N * 4 : 0u);
     float4 sq[QM];
 #pragma unroll
     for (int m = 0; m < QM; ++m) {
@@ -343,11 +357,14 @@ __global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
         sq[m] = buf_load4(rs, q < Q ? (uint32_t)q * 16u : kBufferOob);
     }
     const bool col = tid < N;
-    const uint32_t off = col ? (uint32_t)tid * 4u : kBufferOob;
+    const uint32_t off = col && live ? (uint32_t)tid * 4u : kBufferOob;
     const float rv = buf_load(make_rsrc(p.r + base, N * 4), off);
-    const float wv = buf_load(make_rsrc(p.w + base, N * 4), off);
+    float wv = 0.0f, av = 0.0f;
+    if constexpr (!LR) {
+        wv = buf_load(make_rsrc(p.w + base, N * 4), off);
+        av = buf_load(make_rsrc(p.a + base, N * 4), off);
+    }
     float kv = buf_load(make_rsrc(p.k + base, N * 4), off);
-    float av = buf_load(make_rsrc(p.a + base, N * 4), off);
     const float vv = buf_load(make_rsrc(p.v + base, N * 4), off);
     float bv = 0.0f, kk = 0.0f, ka = 0.0f;
     if constexpr (PREP) {
@@ -356,15 +373,91 @@ __global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
     } else {
         bv = buf_load(make_rsrc(p.b + base, N * 4), off);
     }
+    if constexpr (LR) {
+        // Stage the head's weight rows (3 N rows of L, contiguous N x L blocks)
+        // and the streams' rank-L rows: every load is issued before the first
+        // LDS write, so staging costs one memory latency.
+        constexpr int kT = kStepThreads * SPW;
+        constexpr int kW4 = (N * kStepLrMaxL / 4 + kT - 1) / kT;  // float4 per thread and matrix
+        constexpr int kL1 = (SPW * 3 * kStepLrMaxL + kT - 1) / kT;
+        const int L = p.L, nl4 = N * L / 4, flat = threadIdx.x;
+        float4 wreg[3][kW4];
+#pragma unroll
+        for (int m = 0; m < 3; ++m) {
+            const float *src = m == 0 ? p.w2t : (m == 1 ? p.a2t : p.g2t);
+            const auto rw = make_rsrc(src + (size_t)h * N * L, (uint32_t)(N * L * 4));
+#pragma unroll
+            for (int i = 0; i < kW4; ++i) {
+                const int e4 = flat + i * kT;
+                wreg[m][i] = buf_load4(rw, e4 < nl4 ? (uint32_t)e4 * 16u : kBufferOob);
+            }
+        }
+        float lreg[kL1];
+#pragma unroll
+        for (int i = 0; i < kL1; ++i) {
+            const int e = flat + i * kT;
+            const int sb = e / (3 * L), rem = e - sb * 3 * L, m = rem / L, j = rem - m * L;
+            const int b2 = (blockIdx.x / p.H) * SPW + sb;
+            const bool ok = sb < SPW && b2 < p.B;
+            lreg[i] = ok ? p.lr[m * p.lr_plane + (size_t)b2 * L + j] : 0.0f;
+        }
+        const float w0c = col ? p.w0[h * N + tid] : 0.0f, a0c = col ? p.a0[h * N + tid] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < 3; ++m)
+#pragma unroll
+            for (int i = 0; i < kW4; ++i) {
+                const int e4 = flat + i * kT;
+                if (e4 < nl4) {
+                    const int c = (4 * e4) / L, j = 4 * e4 - c * L;  // L % 8 == 0
+                    float *dst = &wl[m * N + c][j];
+                    dst[0] = wreg[m][i].x; dst[1] = wreg[m][i].y; dst[2] = wreg[m][i].z; dst[3] = wreg[m][i].w;
+                }
+            }
+#pragma unroll
+        for (int i = 0; i < kL1; ++i) {
+            const int e = flat + i * kT;
+            const int sb = e / (3 * L), rem = e - sb * 3 * L, m = rem / L, j = rem - m * L;
+            if (sb < SPW) lrs[sb][m][j] = lreg[i];
+        }
+        lds_barrier();
+        // One dot per thread (PAIR = false) or per lane pair, the even and odd
+        // j of a dot on lanes 2q and 2q + 1, summed through a DPP swap.
+        constexpr bool PAIR = 6 * N <= kStepThreads;
+        constexpr int TPD = PAIR ? 2 : 1;
+        if (tid < 3 * N * TPD) {
+            const int dq = tid / TPD, hj = tid % TPD, m = dq / N, c = dq - m * N;
+            const float *wrow = &wl[m * N + c][hj];
+            const float *lrow = &lrs[sub][m][hj];
+            float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 4
+            for (int i = 0; i < L / TPD; i += 4)  // L % 8 == 0
+#pragma unroll
+                for (int t = 0; t < 4; ++t) acc[t] = fmaf(lrow[TPD * (i + t)], wrow[TPD * (i + t)], acc[t]);
+            float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+            if constexpr (PAIR) dot += dpp_move<dpp::kQuadXor1>(dot);
+            if (hj == 0) {
+                if (m == 2) {
+                    if (live) p.g_out[(size_t)bb * p.H * N + h * N + c] = 1.0f / (1.0f + expf(-dot));
+                } else {
+                    lrv[sub][m][c] = dot;
+                }
+            }
+        }
+        lds_barrier();
+        if (col) {
+            wv = w0c + lrv[sub][0][tid];
+            av = 1.0f / (1.0f + expf(-(a0c + lrv[sub][1][tid])));
+        }
+    }
     if constexpr (PREP) {
         // kappa = normalize(k * k_k) over the head (F.normalize, eps 1e-12).
         const float x = kv * kk;
         const float ws = wave_sum(x * x);
-        if (lane == 0) red[wave] = ws;
+        if (lane == 0) red[sub][wave] = ws;
         lds_barrier();
         float sq2 = 0.0f;
 #pragma unroll
-        for (int w = 0; w < (N + 63) / 64; ++w) sq2 += red[w];
+        for (int w = 0; w < (N + 63) / 64; ++w) sq2 += red[sub][w];
         const float inv = 1.0f / fmaxf(sqrtf(sq2), 1e-12f);
         const float kap = x * inv, alpha = av;
         av = -kap;
@@ -374,12 +467,12 @@ __global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
     if (col) {
         // d = exp(-e^{-0.5} sigmoid(w)) = exp2(-e^{-0.5} log2(e) sigmoid(w)).
         const float sig = __frcp_rn(1.0f + __expf(-wv));
-        vec[0][tid] = av;
-        vec[1][tid] = bv;
-        vec[2][tid] = kv;
-        vec[3][tid] = exp2f(-0.8750387749f * sig);
-        vec[4][tid] = rv;
-        vec[5][tid] = vv;
+        vec[sub][0][tid] = av;
+        vec[sub][1][tid] = bv;
+        vec[sub][2][tid] = kv;
+        vec[sub][3][tid] = exp2f(-0.8750387749f * sig);
+        vec[sub][4][tid] = rv;
+        vec[sub][5][tid] = vv;
     }
     lds_barrier();
     // sa_i = sum_j S_ij a_j.
@@ -387,45 +480,46 @@ __global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
     for (int m = 0; m < QM; ++m) {
         const int q = tid + m * kStepThreads;
         if (q < Q) {
-            const float4 a4 = *reinterpret_cast<const float4 *>(&vec[0][(4 * q) % N]);
-            part[q] = (sq[m].x * a4.x + sq[m].y * a4.y) + (sq[m].z * a4.z + sq[m].w * a4.w);
+            const float4 a4 = *reinterpret_cast<const float4 *>(&vec[sub][0][(4 * q) % N]);
+            part[sub][q] = (sq[m].x * a4.x + sq[m].y * a4.y) + (sq[m].z * a4.z + sq[m].w * a4.w);
         }
     }
     lds_barrier();
     if (tid < N) {
         float sa = 0.0f;
 #pragma unroll
-        for (int u = 0; u < RQ; ++u) sa += part[tid * RQ + u];
-        rowv[tid] = sa;
+        for (int u = 0; u < RQ; ++u) sa += part[sub][tid * RQ + u];
+        rowv[sub][tid] = sa;
     }
     lds_barrier();
     // S'_ij = S_ij d_j + sa_i b_j + v_i k^_j;  y_i = sum_j S'_ij r_j.
-    const auto ro = make_rsrc(p.state_out ? p.state_out + state_off : nullptr, p.state_out ? N * N * 4 : 0u);
+    const auto ro = make_rsrc(live && p.state_out ? p.state_out + state_off : nullptr,
+                              live && p.state_out ? N * N * 4 : 0u);
 #pragma unroll
     for (int m = 0; m < QM; ++m) {
         const int q = tid + m * kStepThreads;
         if (q < Q) {
             const int i = (4 * q) / N, c = (4 * q) % N;
-            const float sa = rowv[i], vi = vec[5][i];
-            const float4 b4 = *reinterpret_cast<const float4 *>(&vec[1][c]);
-            const float4 k4 = *reinterpret_cast<const float4 *>(&vec[2][c]);
-            const float4 d4 = *reinterpret_cast<const float4 *>(&vec[3][c]);
-            const float4 r4 = *reinterpret_cast<const float4 *>(&vec[4][c]);
+            const float sa = rowv[sub][i], vi = vec[sub][5][i];
+            const float4 b4 = *reinterpret_cast<const float4 *>(&vec[sub][1][c]);
+            const float4 k4 = *reinterpret_cast<const float4 *>(&vec[sub][2][c]);
+            const float4 d4 = *reinterpret_cast<const float4 *>(&vec[sub][3][c]);
+            const float4 r4 = *reinterpret_cast<const float4 *>(&vec[sub][4][c]);
             float4 x;
             x.x = fmaf(sq[m].x, d4.x, fmaf(sa, b4.x, k4.x * vi));
             x.y = fmaf(sq[m].y, d4.y, fmaf(sa, b4.y, k4.y * vi));
             x.z = fmaf(sq[m].z, d4.z, fmaf(sa, b4.z, k4.z * vi));
             x.w = fmaf(sq[m].w, d4.w, fmaf(sa, b4.w, k4.w * vi));
-            part[q] = (x.x * r4.x + x.y * r4.y) + (x.z * r4.z + x.w * r4.w);
+            part[sub][q] = (x.x * r4.x + x.y * r4.y) + (x.z * r4.z + x.w * r4.w);
             if (p.state_out)
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), ro, (uint32_t)q * 16u, 0, 0);
         }
     }
     lds_barrier();
-    if (tid < N) {
+    if (tid < N && live) {
         float yv = 0.0f;
 #pragma unroll
-        for (int u = 0; u < RQ; ++u) yv += part[tid * RQ + u];
+        for (int u = 0; u < RQ; ++u) yv += part[sub][tid * RQ + u];
         p.y[base + tid] = yv;
     }
 }
@@ -433,11 +527,21 @@ __global__ void __launch_bounds__(kStepThreads) wkv7_step_kernel(WkvParams p) {
 template <int N>
 hipError_t launch_step_n(const WkvParams &p, bool prep, hipStream_t stream) {
     static_assert(N % 4 == 0 && N <= kStepThreads, "step kernel layout");
+    if (p.lr) {
+        if constexpr (3 * N <= kStepThreads) {
+            if (!prep || !wkv7_step_lowrank_ok(N, p.L)) return hipErrorInvalidValue;
+            const dim3 grid(((p.B + kStepLrSpw - 1) / kStepLrSpw) * p.H), block(kStepThreads * kStepLrSpw);
+            hipLaunchKernelGGL((wkv7_step_kernel<N, true, kStepLrSpw, true>), grid, block, 0, stream, p);
+            return hipGetLastError();
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
     const dim3 grid(p.B * p.H), block(kStepThreads);
     if (prep)
-        hipLaunchKernelGGL((wkv7_step_kernel<N, true>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((wkv7_step_kernel<N, true, 1, false>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL((wkv7_step_kernel<N, false>), grid, block, 0, stream, p);
+        hipLaunchKernelGGL((wkv7_step_kernel<N, false, 1, false>), grid, block, 0, stream, p);
     return hipGetLastError();
 }
 
@@ -457,6 +561,11 @@ hipError_t launch_n(const WkvParams &p, bool prep, hipStream_t stream) {
 
 }  // namespace
 
+bool wkv7_step_lowrank_ok(int N, int L) {
+    return (N == 8 || N == 16 || N == 32 || N == 40 || N == 48 || N == 64) && L >= 8 && L <= kStepLrMaxL &&
+           L % 8 == 0;
+}
+
 bool wkv7_supported(int N) {
     return N == 8 || N == 16 || N == 32 || N == 40 || N == 48 || N == 64 || N == 128;
 }
@@ -466,7 +575,9 @@ hipError_t launch_wkv7(const WkvParams &p, int N, bool prep, hipStream_t stream)
     const char *force = std::getenv("YUF_WKV7_KERNEL");
     const bool want_serial = force && std::strcmp(force, "serial") == 0;
     const bool want_chunked = force && std::strcmp(force, "chunked") == 0;
-    if (wkv7_chunk_supported(N) && !want_serial && (want_chunked || p.T >= kWkvChunkMinT))
+    // The fused low-rank form is the single-token step kernel only.
+    if (p.lr && (p.T != 1 || !prep)) return hipErrorInvalidValue;
+    if (!p.lr && wkv7_chunk_supported(N) && !want_serial && (want_chunked || p.T >= kWkvChunkMinT))
         return launch_wkv7_chunked(p, N, prep, stream);
     switch (N) {
         case 8: return launch_n<8>(p, prep, stream);
