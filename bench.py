@@ -253,10 +253,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5", "kernels"], default=None,
+    ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5", "kernels", "gemm"], default=None,
                     help="profiling aids: just the C2 scan (20 launches), just the prefill steps, just the C4 "
-                         "decode leg, or a plain 256 MiB device copy (20 launches) that calibrates the "
-                         "FETCH_SIZE/WRITE_SIZE counters")
+                         "decode leg, a plain 256 MiB device copy (20 launches) that calibrates the "
+                         "FETCH_SIZE/WRITE_SIZE counters, the three HBM-bound kernel legs, or the FFN "
+                         "projection GEMM alone (11 launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -271,6 +272,9 @@ def main() -> int:
     if args.only == "kernels":  # the three HBM-bound kernel legs, for one profiling run
         print(json.dumps({"roofline": bench_scan(20), "decode_roofline": bench_wkv_step(50),
                           "rosa_roofline": bench_rosa(20)}), flush=True)
+        return 0
+    if args.only == "gemm":
+        print(json.dumps({"gemm_roofline": bench_gemm(10)}), flush=True)
         return 0
     if args.only == "copy":
         src = torch.ones(64 << 20, device="cuda")
