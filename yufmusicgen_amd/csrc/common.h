@@ -84,11 +84,9 @@ __device__ __forceinline__ double dpp_move_f64(double x) {
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-__device__ __forceinline__ double wave_sum_f64(double x) {
-    x += dpp_move_f64<dpp::kQuadXor1>(x);
-    x += dpp_move_f64<dpp::kQuadXor2>(x);
-    x += dpp_move_f64<dpp::kRowHalfMirror>(x);
-    x += dpp_move_f64<dpp::kRowMirror>(x);
+// Sum over the four lanes l % 16 == const (one per 16-lane row), returned to
+// those four lanes with the same bits.
+__device__ __forceinline__ double rows_sum_f64(double x) {
     uint64_t b = __builtin_bit_cast(uint64_t, x);
     const auto l16 = __builtin_amdgcn_permlane16_swap((uint32_t)b, (uint32_t)b, false, false);
     const auto h16 = __builtin_amdgcn_permlane16_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
@@ -99,6 +97,14 @@ __device__ __forceinline__ double wave_sum_f64(double x) {
     const auto h32 = __builtin_amdgcn_permlane32_swap((uint32_t)(b >> 32), (uint32_t)(b >> 32), false, false);
     return __builtin_bit_cast(double, ((uint64_t)h32[0] << 32) | l32[0]) +
            __builtin_bit_cast(double, ((uint64_t)h32[1] << 32) | l32[1]);
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+    x += dpp_move_f64<dpp::kQuadXor1>(x);
+    x += dpp_move_f64<dpp::kQuadXor2>(x);
+    x += dpp_move_f64<dpp::kRowHalfMirror>(x);
+    x += dpp_move_f64<dpp::kRowMirror>(x);
+    return rows_sum_f64(x);
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }

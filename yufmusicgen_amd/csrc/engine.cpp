@@ -43,6 +43,7 @@ struct LayerW {
     const float *rosa_w3, *rosa_b3, *rosa_hh, *rosa_decay, *rosa_out;
     const float *ln_f_w, *ln_f_b, *ffn_cat, *ffn_out;
     const float *rosa_al;  // A^kRosaSeg of the ROSA transition, [D][D] row-major
+    const float *rosa_u, *rosa_lam;  // u = normalize(householder), lambda = sigmoid(decay), [D]
 };
 
 // Segment length of the segmented ROSA prefill scan.
@@ -77,9 +78,11 @@ struct Engine {
           *ffn = nullptr, *hl = nullptr;
     float *rz = nullptr, *rcarry = nullptr, *rends = nullptr;  // segmented ROSA scratch
     bool rosa_segmented = true;                                // YUF_ROSA_SEGMENTED=0 disables
+    bool decode_fusion = true;                                 // YUF_DECODE_FUSION=0: separate low-rank GEMM and ROSA step
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
     size_t gemm_ws_floats = 0;
     int *slots_dev = nullptr, *tokens_dev = nullptr, *bad_dev = nullptr;
+    int *rosa_count = nullptr;  // [max_streams]: 16-row tile counters of the fused ROSA-out kernel, by first stream
     int *slots_host = nullptr;  // pinned
     std::vector<int> last_slots;
     // Device staging for the host-buffer entry points (grown on demand).
@@ -270,6 +273,13 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
                 for (long long i = 0; i < D; ++i) al[(size_t)(i * D + j)] = (float)x[(size_t)i];
             }
             append(al.data(), al.size());
+            std::vector<float> uf((size_t)D), lf((size_t)D);
+            for (long long j = 0; j < D; ++j) {
+                uf[(size_t)j] = (float)u[(size_t)j];
+                lf[(size_t)j] = (float)lam[(size_t)j];
+            }
+            append(uf.data(), uf.size());
+            append(lf.data(), lf.size());
         }
     }
     return YUF_OK;
@@ -335,6 +345,7 @@ struct Act {
     float *h, *xn, *mix, *r, *k, *v, *wr, *al, *g, *lr, *y, *z, *rosa3, *rread, *ffn, *hl;
     float *rz, *rcarry, *rends;  // segmented ROSA scratch (segment rows of kRosaSeg tokens)
     const int *tokens, *slots;
+    int *rcount;  // fused ROSA-out tile counters of this group of streams
 };
 
 Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
@@ -353,6 +364,7 @@ Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
     a.rz = e.rz + seg0; a.rcarry = e.rcarry + seg0; a.rends = e.rends + seg0;
     a.tokens = e.tokens_dev + m0;
     a.slots = e.slots_dev + s0;
+    a.rcount = e.rosa_count + s0;
     return a;
 }
 
@@ -394,7 +406,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
                     *ma = a.mix + 4 * plane, *mg = a.mix + 5 * plane;
         int rc;
         // Decode with fp32 weights: the second low-rank stage runs inside the WKV step.
-        const bool fuse_lr = Tc == 1 && !e.w_h && wkv7_step_lowrank_ok(s.head_size, L);
+        const bool fuse_lr = Tc == 1 && e.decode_fusion && !e.w_h && wkv7_step_lowrank_ok(s.head_size, L);
         {
             // r, k, v and the three low-rank first stages (one launch for short
             // products, two otherwise: the tile widths differ); then the second stages.
@@ -436,25 +448,37 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         if ((rc = ln_gemm(e, st, M, 3 * D, d, a.h, d, w.ln_r_w, w.ln_r_b, nullptr, a.xn, w.rosa_w3, a.rosa3, 3 * D,
                           w.rosa_b3)) != YUF_OK)
             return rc;
-        RosaParams rp;
-        rp.B = n; rp.T = Tc; rp.D = D; rp.ld = 3 * D;
-        if (Tc == 1) {
-            // The single-token kernel applies the gates itself.
-            rp.cand = a.rosa3; rp.write = a.rosa3 + D; rp.read_raw = a.rosa3 + 2 * D;
+        if (Tc == 1 && e.decode_fusion && !e.w_h && rosa_out_decode_ok(M, D)) {
+            // Decode: the ROSA step runs as the A prologue of the ROSA-out product.
+            RosaOutParams ro;
+            ro.M = M; ro.N = d; ro.D = D;
+            ro.pre = a.rosa3; ro.ld_pre = 3 * D;
+            ro.mem = ros; ro.mem_rows = e.max_streams; ro.slot = a.slots;
+            ro.u = w.rosa_u; ro.lam = w.rosa_lam; ro.W = w.rosa_out;
+            ro.residual = a.h; ro.ldr = d; ro.C = a.h; ro.ldc = d;
+            ro.counter = a.rcount;
+            ENG_TRY(launch_rosa_out_decode(ro, st), "rosa out (fused step)");
         } else {
-            // Gates on all M rows in parallel, so the sequential scan only loads e and the gate.
-            ENG_TRY(launch_rosa_gates(a.rosa3, M, D, 3 * D, st), "rosa_gates");
-            rp.e_pre = a.rosa3; rp.g_pre = a.rosa3 + D;
+            RosaParams rp;
+            rp.B = n; rp.T = Tc; rp.D = D; rp.ld = 3 * D;
+            if (Tc == 1) {
+                // The single-token kernel applies the gates itself.
+                rp.cand = a.rosa3; rp.write = a.rosa3 + D; rp.read_raw = a.rosa3 + 2 * D;
+            } else {
+                // Gates on all M rows in parallel, so the sequential scan only loads e and the gate.
+                ENG_TRY(launch_rosa_gates(a.rosa3, M, D, 3 * D, st), "rosa_gates");
+                rp.e_pre = a.rosa3; rp.g_pre = a.rosa3 + D;
+            }
+            rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
+            rp.memory_in = ros; rp.memory_out = ros; rp.slot = a.slots; rp.read_out = a.rread;
+            if (e.rosa_segmented && Tc > 1 && rosa_segmented_ok(Tc, D, kRosaSeg)) {
+                ENG_TRY(launch_rosa_segmented(rp, w.rosa_al, kRosaSeg, a.rz, a.rcarry, a.rends, st), "rosa segmented");
+            } else {
+                ENG_TRY(launch_rosa(rp, st), "rosa");
+            }
+            if ((rc = gemm(e, st, M, d, D, a.rread, D, w.rosa_out, D, a.h, d, nullptr, ACT_NONE, a.h, d)) != YUF_OK)
+                return rc;
         }
-        rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
-        rp.memory_in = ros; rp.memory_out = ros; rp.slot = a.slots; rp.read_out = a.rread;
-        if (e.rosa_segmented && Tc > 1 && rosa_segmented_ok(Tc, D, kRosaSeg)) {
-            ENG_TRY(launch_rosa_segmented(rp, w.rosa_al, kRosaSeg, a.rz, a.rcarry, a.rends, st), "rosa segmented");
-        } else {
-            ENG_TRY(launch_rosa(rp, st), "rosa");
-        }
-        if ((rc = gemm(e, st, M, d, D, a.rread, D, w.rosa_out, D, a.h, d, nullptr, ACT_NONE, a.h, d)) != YUF_OK)
-            return rc;
         // FFN
         if ((rc = ln_gemm(e, st, M, 2 * hid, d, a.h, d, w.ln_f_w, w.ln_f_b, nullptr, a.xn, w.ffn_cat, a.ffn, hid,
                           nullptr, nullptr, 0, true)) != YUF_OK)
@@ -662,6 +686,7 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     e.s = s;
     if (const char *ng = std::getenv("YUF_NO_GRAPH")) e.use_graphs = std::strcmp(ng, "1") != 0;
     if (const char *rs = std::getenv("YUF_ROSA_SEGMENTED")) e.rosa_segmented = std::strcmp(rs, "0") != 0;
+    if (const char *df = std::getenv("YUF_DECODE_FUSION")) e.decode_fusion = std::strcmp(df, "0") != 0;
     e.max_streams = max_streams;
     e.max_tokens = max_tokens;
 
@@ -720,6 +745,7 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
         w.rosa_w3 = nxt(); w.rosa_b3 = nxt(); w.rosa_hh = nxt(); w.rosa_decay = nxt(); w.rosa_out = nxt();
         w.ln_f_w = nxt(); w.ln_f_b = nxt(); w.ffn_cat = nxt(); w.ffn_out = nxt();
         w.rosa_al = nxt();
+        w.rosa_u = nxt(); w.rosa_lam = nxt();
     }
 
     // State: [layer][slot][...] for each of prev, wkv, rosa.
@@ -759,16 +785,20 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
                          &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.rends};
         for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
     }
-    const size_t io_bytes = 256 * 3 + (size_t)(max_streams + max_tokens + 1) * sizeof(int);
+    const size_t io_bytes = 256 * 4 + (size_t)(2 * max_streams + max_tokens + 1) * sizeof(int);
     ENG_TRY(hipMalloc(&e.io.p, io_bytes), "io alloc");
     {
         char *cur = static_cast<char *>(e.io.p);
         e.slots_dev = carve<int>(cur, max_streams);
         e.tokens_dev = carve<int>(cur, max_tokens);
         e.bad_dev = carve<int>(cur, 1);
+        e.rosa_count = carve<int>(cur, max_streams);
     }
     ENG_TRY(hipHostMalloc(reinterpret_cast<void **>(&e.slots_host), max_streams * sizeof(int)), "pinned alloc");
     ENG_TRY(hipMemsetAsync(e.bad_dev, 0, sizeof(int), e.stream), "flag clear");
+    // Tile counters of the fused ROSA-out decode kernel: zero here, and every
+    // launch leaves them at zero (outside any captured graph).
+    ENG_TRY(hipMemsetAsync(e.rosa_count, 0, (size_t)max_streams * sizeof(int), e.stream), "counter clear");
     ENG_TRY(hipStreamSynchronize(e.stream), "engine init sync");
     *out = h.release();
     return YUF_OK;

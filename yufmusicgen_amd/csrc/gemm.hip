@@ -213,6 +213,7 @@ __global__ void __launch_bounds__(kThreads) gemm_f32_kernel(GemmGroup g, int per
 // for lane group g on both operands).
 // ---------------------------------------------------------------------------
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // Eight fp32 values (k order) rounded to bf16 for one MFMA operand.
@@ -849,6 +850,130 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
 }
 
 // ---------------------------------------------------------------------------
+// Decode ROSA output projection with the ROSA step as its A prologue.  The
+// unit of work is the decode GEMM's (16-column slice, 16-row tile) with the 8
+// waves splitting K = D (S steps of 16 k per wave); each lane holds 4 k of one
+// row per step.  The step's two projections u.m and u.m' are summed in double
+// (lane partials -> the row's 4 lanes through the row swaps -> the 8 waves in
+// a fixed order through LDS), then the read A[m][k] feeds the MFMAs directly,
+// so the separate step kernel and its read buffer go away.  Every workgroup of
+// a row tile computes the tile's new memory rows; the last one to finish (a
+// device-scope counter per tile, incremented after the tile's reads) stores
+// them in place and resets the counter.  Cross-workgroup traffic is only that
+// counter: the stores never race a read of the old rows.
+template <int S>
+__global__ void __launch_bounds__(kDecThreads) rosa_out_decode_kernel(RosaOutParams p, int mtiles, int units,
+                                                                      int per_xcd) {
+    __shared__ __attribute__((aligned(16))) float red[kDecWaves][16 * 17];
+    __shared__ double pd[2][kDecWaves][16];
+    __shared__ int last;
+    const int u = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (u >= units) return;
+    const int slice = u / mtiles, mt = u - slice * mtiles;
+    const int row0 = mt * 16, rows = min(p.M - row0, 16);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g4 = lane >> 4, li = lane & 15;
+    const bool rv = li < rows;
+    const int slot = rv ? (p.slot ? p.slot[row0 + li] : row0 + li) : 0;
+    const int D = p.D, kw = wave * 16 * S;
+    const auto rm = make_rsrc(p.mem, (uint32_t)((size_t)p.mem_rows * D * 4));
+    const auto rp = make_rsrc(p.pre + (size_t)row0 * p.ld_pre, (uint32_t)(((size_t)(rows - 1) * p.ld_pre + 3 * D) * 4));
+    const auto ru = make_rsrc(p.u, (uint32_t)D * 4u), rl = make_rsrc(p.lam, (uint32_t)D * 4u);
+    const auto rw = make_rsrc(p.W, (uint32_t)((size_t)p.N * D * 4));
+    auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+        return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    };
+    const int wr = slice * 16 + li;
+    floatx4 m[S], e[S], gw[S], rr[S], uu[S], ll[S], b[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int k = kw + 16 * s + 4 * g4;
+        b[s] = load4(rw, wr < p.N ? (uint32_t)((size_t)wr * D + k) * 4u : kBufferOob);
+        m[s] = load4(rm, rv ? (uint32_t)((size_t)slot * D + k) * 4u : kBufferOob);
+        e[s] = load4(rp, rv ? (uint32_t)((size_t)li * p.ld_pre + k) * 4u : kBufferOob);
+        gw[s] = load4(rp, rv ? (uint32_t)((size_t)li * p.ld_pre + D + k) * 4u : kBufferOob);
+        rr[s] = load4(rp, rv ? (uint32_t)((size_t)li * p.ld_pre + 2 * D + k) * 4u : kBufferOob);
+        uu[s] = load4(ru, (uint32_t)k * 4u);
+        ll[s] = load4(rl, (uint32_t)k * 4u);
+    }
+    // Gates (the single-token kernel's expressions): e <- tanh(e) sigmoid(write),
+    // rr <- sigmoid(read_raw); first projection u.m.
+    double f = 0.0;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * e[s][q]) + 1.0f);
+            e[s][q] = th * __frcp_rn(1.0f + __expf(-gw[s][q]));
+            rr[s][q] = __frcp_rn(1.0f + __expf(-rr[s][q]));
+            f = fma((double)uu[s][q], (double)m[s][q], f);
+        }
+    f = rows_sum_f64(f);
+    if (g4 == 0) pd[0][wave][li] = f;
+    lds_barrier();
+    double t = 0.0;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) t += pd[0][w][li];
+    const float p1 = (float)t;
+    double f2 = 0.0;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            m[s][q] = fmaf(ll[s][q], fmaf(-2.0f * p1, uu[s][q], m[s][q]), e[s][q]);
+            f2 = fma((double)uu[s][q], (double)m[s][q], f2);
+        }
+    f2 = rows_sum_f64(f2);
+    if (g4 == 0) pd[1][wave][li] = f2;
+    lds_barrier();
+    t = 0.0;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; ++w) t += pd[1][w][li];
+    const float p2 = (float)t;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        floatx4 a;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) a[q] = fmaf(-2.0f * p2, uu[s][q], m[s][q]) * rr[s][q];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[r], b[s][r], acc, 0, 0, 0);
+    }
+    // Register r of lane l: row 4 (l / 16) + r, column l % 16.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][(4 * g4 + r) * 17 + li] = acc[r];
+    lds_barrier();
+    if (tid < 256) {
+        const int rl = tid >> 4, c = tid & 15, col = slice * 16 + c;
+        if (rl < rows && col < p.N) {
+            float x = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) x += red[w][rl * 17 + c];
+            const int row = row0 + rl;
+            if (p.bias) x += p.bias[col];
+            if (p.residual) x += p.residual[(size_t)row * p.ldr + col];
+            p.C[(size_t)row * p.ldc + col] = x;
+        }
+    }
+    // Every wave has consumed its old memory values (p1 needed them): count
+    // this workgroup; the tile's last one writes the new rows.
+    if (tid == 0) last = atomicAdd(&p.counter[mt], 1) == units / mtiles - 1;
+    lds_barrier();
+    if (last) {
+        if (rv) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int k = kw + 16 * s + 4 * g4;
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, m[s]), rm,
+                                                       (uint32_t)((size_t)slot * D + k) * 4u, 0, 0);
+            }
+        }
+        if (tid == 0) atomicExch(&p.counter[mt], 0);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Short-M path (decode: M <= 64 rows, one token per stream).  The product is
 // bound by streaming W from HBM, so parallelism comes from N and K instead of
 // M: each wave owns 64 rows x 64 columns (2 x 2 MFMA 32x32 tiles) over a K
@@ -1130,6 +1255,23 @@ int skinny_splits(int N, int K) {
 }
 
 }  // namespace
+
+bool rosa_out_decode_ok(int M, int D) { return M >= 1 && M <= 64 && (D == 128 || D == 256); }
+
+hipError_t launch_rosa_out_decode(const RosaOutParams &p, hipStream_t stream) {
+    if (p.M <= 0 || p.N <= 0) return hipSuccess;
+    if (!rosa_out_decode_ok(p.M, p.D) || !p.pre || !p.mem || !p.u || !p.lam || !p.W || !p.C || !p.counter ||
+        p.ld_pre < 3 * p.D || p.mem_rows < 1)
+        return hipErrorInvalidValue;
+    const int mtiles = (p.M + 15) / 16, units = ((p.N + 15) / 16) * mtiles;
+    const int per_xcd = (units + kXcds - 1) / kXcds;
+    const dim3 grid(per_xcd * kXcds), block(kDecThreads);
+    if (p.D == 128)
+        hipLaunchKernelGGL(rosa_out_decode_kernel<1>, grid, block, 0, stream, p, mtiles, units, per_xcd);
+    else
+        hipLaunchKernelGGL(rosa_out_decode_kernel<2>, grid, block, 0, stream, p, mtiles, units, per_xcd);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     if (p.M <= 0 || p.N <= 0) return hipSuccess;

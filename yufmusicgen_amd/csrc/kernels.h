@@ -108,6 +108,34 @@ struct GemmParams {
     int ldg = 0;
 };
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
+
+// Decode ROSA output projection with the ROSA single-token step as its A
+// prologue (M <= 64, fp32 W [N][D], D in {128, 256}): per row m, from the
+// memory row mem[slot[m]] and the pre-activations e | write | read_raw at
+// pre + m * ld_pre,
+//   m' = lambda (m - 2 (u.m) u) + tanh(e) sigmoid(write),
+//   A[m] = (m' - 2 (u.m') u) sigmoid(read_raw),
+// then C = A W^T (+ bias) (+ residual).  The last workgroup of each 16-row tile
+// to finish (counter[tile], left at zero) writes m' back to mem[slot[m]], after
+// every workgroup of the tile has read the old row.
+struct RosaOutParams {
+    int M = 0, N = 0, D = 0;
+    const float *pre = nullptr;
+    int ld_pre = 0;
+    float *mem = nullptr;
+    int mem_rows = 0;
+    const int *slot = nullptr;
+    const float *u = nullptr, *lam = nullptr;  // unit direction, sigmoid(decay) [D]
+    const float *W = nullptr;
+    const float *bias = nullptr;
+    const float *residual = nullptr;
+    int ldr = 0;
+    float *C = nullptr;
+    int ldc = 0;
+    int *counter = nullptr;  // ceil(M / 16) ints, zero between launches
+};
+bool rosa_out_decode_ok(int M, int D);
+hipError_t launch_rosa_out_decode(const RosaOutParams &p, hipStream_t stream);
 // Up to kMaxGroup independent products in one launch (M > 64: one launch for
 // the group; M <= 64: one launch per SiLU flag and prologue kind).
 constexpr int kMaxGroup = 6;
