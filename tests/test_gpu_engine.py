@@ -14,7 +14,7 @@ import torch
 
 from oracle.model import OracleModel, blob_to_state, state_to_blob
 from yufmusicgen_amd.checkpoint import write_yuf
-from yufmusicgen_amd.config import PRESETS
+from yufmusicgen_amd.config import PRESETS, ModelConfig
 from yufmusicgen_amd.engine import Checkpoint, Engine, sample_device
 from yufmusicgen_amd.synth import prompt_tokens, synth_weights, uniform_tokens
 
@@ -391,3 +391,32 @@ def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, pre
     for t in range(3):  # host-buffer entry point (also graph-replayed)
         ids = steps[:, t]
         np.testing.assert_array_equal(graph_eng.step(ids), eager_eng.step(ids))
+
+
+@pytest.mark.parametrize("preset,n", [("0.1b", 40), ("d256_rosa256", 5)])
+def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n):
+    """The folded decode kernels (second low-rank stage inside the WKV step,
+    ROSA step as the ROSA-out prologue with the tile's last workgroup writing
+    the memory) against the separate kernels (YUF_DECODE_FUSION=0): logits and
+    every carried state over several steps, with slots permuted so the ROSA
+    rows are gathered and scattered through the slot map."""
+    # d256_rosa256: head size 64 and ROSA 256 (two 16-k steps per wave) on a small model.
+    cfg = PRESETS[preset] if preset in PRESETS else ModelConfig(
+        vocab_size=512, d_model=256, n_layers=2, n_heads=4, head_size=64, rosa_size=256)
+    weights = synth_weights(cfg, seed=11)
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, weights)
+    ck = Checkpoint.load(path)
+    slots = np.random.default_rng(5).permutation(n + 3)[:n].astype(np.int32)
+    prompt = uniform_tokens(12, n, 5, cfg.vocab_size)
+    steps = uniform_tokens(13, n, 4, cfg.vocab_size)
+    out = {}
+    for fusion in ("1", "0"):
+        monkeypatch.setenv("YUF_DECODE_FUSION", fusion)
+        eng = Engine(ck, max_streams=n + 3, max_tokens=n * 5)
+        eng.prefill(prompt, slots=slots, logits="none")
+        logits = [eng.step(steps[:, t], slots=slots) for t in range(steps.shape[1])]
+        out[fusion] = (np.stack(logits), _states_from_blob(eng, slots))
+        eng.close()
+    np.testing.assert_allclose(out["1"][0], out["0"][0], rtol=0, atol=1e-4)
+    np.testing.assert_allclose(out["1"][1], out["0"][1], rtol=1e-4, atol=1e-5)
