@@ -1204,18 +1204,16 @@ hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
         }
         return hipSuccess;
     }
-    int units1 = 0, spw = 1, mrows = 0;
+    int units1 = 0, spw = 1;
     for (int i = 0; i < count; ++i) {
         const GemmParams &p = ps[i];
         const int slices = p.silu_pair ? p.N / 32 : (p.N + 15) / 16;
         units1 += slices * ((p.M + 15) / 16);
         spw = std::max(spw, ((p.K + KS - 1) / KS + kDecWaves - 1) / kDecWaves);
-        mrows = std::max(mrows, p.M);
     }
     // Wide products (the LM head) already fill the chip with 64-row tiles.
     // (Measured: the LN + SiLU-pair FFN input is slower with them, 17.7 against
     // 15.1 us at 64 x 5120 x 640, so it keeps 16-row tiles.)
-    (void)mrows;
     const int MI = (units1 > 1024 && PRO < 2 && !(PRO == 1 && NT == 2)) ? 4 : 1;
     DecodeGroup g{};
     g.count = count;
