@@ -30,7 +30,10 @@ def run_linear(a, w, bias=None, act=0, residual=None):
                                    (300, 640, 100), (512, 512, 36), (1000, 160, 640), (700, 1280, 64),
                                    (2048, 640, 2560), (640, 384, 640), (512, 64, 640), (300, 192, 100),
                                    # decode path (M <= 64): column tails, short K, long K
-                                   (64, 5120, 640), (37, 100, 36), (64, 640, 2560), (1, 20480, 640), (16, 64, 64)])
+                                   (64, 5120, 640), (37, 100, 36), (64, 640, 2560), (1, 20480, 640), (16, 64, 64),
+                                   # wide decode products (A held in registers across >= 512 slices): the
+                                   # LM head shape, row tails, a column tail, short K
+                                   (64, 20480, 640), (33, 20480, 640), (40, 8200, 36), (48, 10000, 100)])
 def test_linear_matches_float64(m, n, k):
     print(f"linear {m}x{n}x{k}", flush=True)
     rng = np.random.default_rng(m + n + k)
@@ -42,7 +45,8 @@ def test_linear_matches_float64(m, n, k):
 
 
 @pytest.mark.parametrize("act", [0, 1, 2])
-@pytest.mark.parametrize("m,n", [(150, 70), (384, 320), (260, 512), (300, 384), (257, 64), (48, 70), (64, 640)])
+@pytest.mark.parametrize("m,n", [(150, 70), (384, 320), (260, 512), (300, 384), (257, 64), (48, 70), (64, 640),
+                                 (48, 8200)])
 def test_linear_epilogues(act, m, n):
     rng = np.random.default_rng(act)
     a = rng.standard_normal((m, 96)).astype(np.float32)
@@ -56,11 +60,14 @@ def test_linear_epilogues(act, m, n):
 
 @pytest.mark.parametrize("m,n,k,gated", [(64, 640, 640, False), (64, 640, 640, True), (37, 384, 640, False),
                                          (5, 100, 36, True), (64, 1280, 1024, False), (64, 640, 1024, True),
-                                         (64, 9000, 640, False), (20, 48, 1024, True)])
+                                         (64, 9000, 640, False), (20, 48, 1024, True), (33, 20480, 640, False),
+                                         (20, 9000, 640, False)])
 def test_ln_linear_matches_float64(m, n, k, gated):
     """LayerNorm (-> gate) -> Linear in one decode kernel.  K = 1024 with a gate,
-    and the 9000-wide product (64-row tiles), take the statistics pass that
-    re-reads the rows; the others reuse the A values already loaded."""
+    and the 9000-wide product at 20 rows (64-row tiles), take the statistics
+    pass that re-reads the rows; the 9000- and 20480-wide products at 33-64
+    rows run the wide kernel (LayerNorm applied once to the A rows held in
+    registers); the others reuse the A values already loaded."""
     print(f"ln_linear {m}x{n}x{k} gate={gated}", flush=True)
     rng = np.random.default_rng(m * 7 + n + k)
     a = (rng.standard_normal((m, k)) * 2.0 + 0.5).astype(np.float32)

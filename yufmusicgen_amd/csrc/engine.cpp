@@ -318,7 +318,8 @@ int gemm(Engine &e, hipStream_t st, int M, int N, int K, const float *A, int lda
 int ln_gemm(Engine &e, hipStream_t st, int M, int N, int K, const float *A, int lda, const float *gamma,
             const float *beta, const float *gate, float *scratch, const float *W, float *C, int ldc,
             const float *bias = nullptr, const float *residual = nullptr, int ldr = 0, bool silu_pair = false) {
-    if (M <= 64 && K % 4 == 0 && K <= 1024 && N <= 8192) {
+    // Wide N fuses only where the wide decode kernel runs (fp32 W, 32 < M, K <= 640).
+    if (M <= 64 && K % 4 == 0 && K <= 1024 && (N <= 8192 || (M > 32 && K <= 640 && !e.w_h))) {
         GemmParams p = make_gemm(e, M, N, K, A, lda, W, K, C, ldc, bias, ACT_NONE, residual, ldr, silu_pair);
         p.ln_gamma = gamma; p.ln_beta = beta; p.a_gate = gate; p.ldg = gate ? lda : 0;
         ENG_TRY(launch_gemm(p, st), "ln gemm");

@@ -850,6 +850,149 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
 }
 
 // ---------------------------------------------------------------------------
+// Wide decode products (the LM head: M <= 64, far more 16-column slices than
+// CUs, K <= 640, fp32 W).  The decode kernel above re-reads the 64 x K block of
+// A once per slice (1,280 times for the LM head); here one workgroup per CU
+// keeps its 8 waves' K ranges of all 64 rows in registers (S steps of 16 k;
+// LayerNorm applied there once) and walks the slices g, g + G, ...: the next
+// slice's W is in flight during the current slice's MFMAs, and the 8 partial
+// tiles are summed through two alternating LDS buffers (one barrier a slice).
+template <int S, bool LN>
+__global__ void __launch_bounds__(kDecThreads) gemm_wide_kernel(GemmParams p, int slices) {
+    __shared__ __attribute__((aligned(16))) float red[2][kDecWaves][64 * 17];
+    __shared__ float part[2][kDecWaves][LN ? 64 : 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g4 = lane >> 4, li = lane & 15;
+    const int K = p.K, M = p.M, k0 = wave * 16 * S;
+    const auto ra = make_rsrc(p.A, (uint32_t)(((size_t)(M - 1) * p.lda + K) * 4));
+    const auto rw = make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + K) * 4));
+    auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+        return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    };
+    floatx4 a[S][4];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = k0 + 16 * s + 4 * g4, row = 16 * i + li;
+            a[s][i] = load4(ra, row < M && k < K ? (uint32_t)((size_t)row * p.lda + k) * 4u : kBufferOob);
+        }
+    floatx4 b0[S], b1[S];
+    auto load_w = [&](floatx4 (&b)[S], int slice) {
+        const int wr = slice * 16 + li;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int k = k0 + 16 * s + 4 * g4;
+            b[s] = load4(rw, slice < slices && wr < p.N && k < K ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob);
+        }
+    };
+    int j = blockIdx.x;
+    if constexpr (LN) {
+        floatx4 gm[S], bt[S];
+        const auto rg = make_rsrc(p.ln_gamma, (uint32_t)K * 4u), rb = make_rsrc(p.ln_beta, (uint32_t)K * 4u);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int k = k0 + 16 * s + 4 * g4;
+            gm[s] = load4(rg, k < K ? (uint32_t)k * 4u : kBufferOob);
+            bt[s] = load4(rb, k < K ? (uint32_t)k * 4u : kBufferOob);
+        }
+        load_w(b0, j);
+        // Row statistics (two passes, the decode kernel's expressions).
+        float mean[4], rstd[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float ps = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s) ps += (a[s][i][0] + a[s][i][1]) + (a[s][i][2] + a[s][i][3]);
+            ps += __shfl_xor(ps, 16);
+            ps += __shfl_xor(ps, 32);
+            if (g4 == 0) part[0][wave][16 * i + li] = ps;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) sum += part[0][w][16 * i + li];
+            mean[i] = sum / (float)K;
+            float sq = 0.0f;
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+                if (k0 + 16 * s + 4 * g4 < K) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const float dv = a[s][i][q] - mean[i];
+                        sq = fmaf(dv, dv, sq);
+                    }
+                }
+            sq += __shfl_xor(sq, 16);
+            sq += __shfl_xor(sq, 32);
+            if (g4 == 0) part[1][wave][16 * i + li] = sq;
+        }
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float sq = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kDecWaves; ++w) sq += part[1][w][16 * i + li];
+            rstd[i] = rsqrtf(sq / (float)K + 1e-5f);
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const bool kin = k0 + 16 * s + 4 * g4 < K;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    a[s][i][q] = kin ? (a[s][i][q] - mean[i]) * rstd[i] * gm[s][q] + bt[s][q] : 0.0f;
+        }
+    } else {
+        load_w(b0, j);
+    }
+    // One slice: MFMAs on b, the 8 partial tiles through red[RB], the epilogue.
+    auto slice_step = [&](const floatx4 (&b)[S], int slice, float (*rbuf)[64 * 17]) {
+        floatx4 acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s][i][r], b[s][r], acc[i], 0, 0, 0);
+        // Register r of lane l in m-tile i: row 16 i + 4 (l / 16) + r, column l % 16.
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) rbuf[wave][(16 * i + 4 * g4 + r) * 17 + li] = acc[i][r];
+        lds_barrier();
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int q = tid + e * kDecThreads, rl = q >> 4, c = q & 15, col = slice * 16 + c;
+            if (rl < M && col < p.N) {
+                float x = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kDecWaves; ++w) x += rbuf[w][rl * 17 + c];
+                float y = apply_act(x + (p.bias ? p.bias[col] : 0.0f), p.act);
+                if (p.residual) y += p.residual[(size_t)rl * p.ldr + col];
+                p.C[(size_t)rl * p.ldc + col] = y;
+            }
+        }
+    };
+    const int G = gridDim.x;
+    while (j < slices) {
+        load_w(b1, j + G);
+        slice_step(b0, j, red[0]);
+        j += G;
+        if (j >= slices) break;
+        load_w(b0, j + G);
+        slice_step(b1, j, red[1]);
+        j += G;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode ROSA output projection with the ROSA step as its A prologue.  The
 // unit of work is the decode GEMM's (16-column slice, 16-row tile) with the 8
 // waves splitting K = D (S steps of 16 k per wave); each lane holds 4 k of one
@@ -1254,6 +1397,36 @@ int skinny_splits(int N, int K) {
 
 }  // namespace
 
+// The wide form: single plain or LN-prologue products, fp32 W, 32 < M <= 64,
+// K <= 640, at least 512 slices (the LM head).
+static int wide_steps(const GemmParams &p) {
+    if (p.Wh || p.silu_pair || p.a_gate || p.M <= 32 || p.M > 64 || p.K % 4 != 0 || p.K > 640) return 0;
+    if ((p.N + 15) / 16 < 512) return 0;
+    return ((p.K + 15) / 16 + kDecWaves - 1) / kDecWaves;
+}
+
+template <int S>
+static void launch_wide_s(const GemmParams &p, int slices, hipStream_t stream) {
+    const dim3 grid(std::min(slices, 256)), block(kDecThreads);
+    if (p.ln_gamma)
+        hipLaunchKernelGGL((gemm_wide_kernel<S, true>), grid, block, 0, stream, p, slices);
+    else
+        hipLaunchKernelGGL((gemm_wide_kernel<S, false>), grid, block, 0, stream, p, slices);
+}
+
+static hipError_t launch_wide(const GemmParams &p, int steps, hipStream_t stream) {
+    const int slices = (p.N + 15) / 16;
+    switch (steps) {
+        case 1: launch_wide_s<1>(p, slices, stream); break;
+        case 2: launch_wide_s<2>(p, slices, stream); break;
+        case 3: launch_wide_s<3>(p, slices, stream); break;
+        case 4: launch_wide_s<4>(p, slices, stream); break;
+        case 5: launch_wide_s<5>(p, slices, stream); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 bool rosa_out_decode_ok(int M, int D) { return M >= 1 && M <= 64 && (D == 128 || D == 256); }
 
 hipError_t launch_rosa_out_decode(const RosaOutParams &p, hipStream_t stream) {
@@ -1278,6 +1451,7 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     // Buffer descriptors address at most 2^31 bytes per 128-row panel.
     if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
     if (!prologue_ok(p)) return hipErrorInvalidValue;
+    if (const int ws = wide_steps(p)) return launch_wide(p, ws, stream);
     if (decode_ok(p)) return launch_decode(&p, 1, stream);
     if (p.Wh) return launch_gemm_group(&p, 1, stream);  // bf16 W: large-tile path or an error
     if (p.M <= 64) {
