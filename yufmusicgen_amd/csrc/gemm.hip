@@ -850,7 +850,8 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
 }
 
 // ---------------------------------------------------------------------------
-// Wide decode products (the LM head: M <= 64, far more 16-column slices than
+// Wide decode products (the LM head, yufmusicgen/model.py:421
+// lm_head(final_norm(hidden)): M <= 64, far more 16-column slices than
 // CUs, K <= 640, fp32 W).  The decode kernel above re-reads the 64 x K block of
 // A once per slice (1,280 times for the LM head); here one workgroup per CU
 // keeps its 8 waves' K ranges of all 64 rows in registers (S steps of 16 k;
@@ -993,7 +994,9 @@ __global__ void __launch_bounds__(kDecThreads) gemm_wide_kernel(GemmParams p, in
 }
 
 // ---------------------------------------------------------------------------
-// Decode ROSA output projection with the ROSA step as its A prologue.  The
+// Decode ROSA output projection with the ROSA step as its A prologue
+// (yufmusicgen/model.py:296-311: output(H(m_t) * sigmoid(read_gate)), the step
+// of yufmusicgen/cuda/rosa_householder.cu:63-101 for T = 1).  The
 // unit of work is the decode GEMM's (16-column slice, 16-row tile) with the 8
 // waves splitting K = D (S steps of 16 k per wave); each lane holds 4 k of one
 // row per step.  The step's two projections u.m and u.m' are summed in double
