@@ -48,14 +48,15 @@ constexpr int kPoolCap = 1024;
 
 // Fallback selection (many ties at the bound): 4-pass 8-bit radix select of the
 // k-th largest key, then the keys above it and ties up to k in arrival order.
+template <int NTH>
 __device__ void radix_topk(const float *row, int V, int k, int tid, uint32_t *hist, uint32_t &sh_prefix,
                            uint32_t &sh_remaining, uint32_t &sh_gt, uint32_t &sh_eq, float *cand_val, int *cand_idx) {
     uint32_t prefix = 0, mask = 0;
     if (tid == 0) sh_remaining = (uint32_t)k;
     for (int shift = 24; shift >= 0; shift -= 8) {
-        hist[tid] = 0;
+        for (int hb = tid; hb < 256; hb += NTH) hist[hb] = 0;
         __syncthreads();
-        for (int i = tid; i < V; i += kThreads) {
+        for (int i = tid; i < V; i += NTH) {
             const uint32_t key = order_key(row[i]);
             if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
         }
@@ -79,7 +80,7 @@ __device__ void radix_topk(const float *row, int V, int k, int tid, uint32_t *hi
     __syncthreads();
     const uint32_t n_eq = sh_remaining;
     const uint32_t n_gt = (uint32_t)k - n_eq;
-    for (int i = tid; i < V; i += kThreads) {
+    for (int i = tid; i < V; i += NTH) {
         const float x = row[i];
         const uint32_t key = order_key(x);
         if (key > prefix) {
@@ -92,17 +93,22 @@ __device__ void radix_topk(const float *row, int V, int k, int tid, uint32_t *hi
     }
 }
 
-constexpr int kRegF4 = 24;  // float4 per thread when the row is held in registers (V <= 24576)
+constexpr int kRegElems = 24576;  // rows up to this many logits are held in registers
+constexpr int kRegThreads = 1024;  // threads per row on that path (four waves per SIMD)
 
-template <bool REG>
-__global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *logits, float temperature, int top_k,
-                                                         uint64_t seed, uint64_t counter, int32_t *tokens) {
+template <int NTH, bool REG>
+__global__ void __launch_bounds__(NTH) sample_kernel(int V, const float *logits, float temperature, int top_k,
+                                                    uint64_t seed, uint64_t counter, int32_t *tokens) {
+    static_assert(NTH % kThreads == 0, "bound groups of NTH / 256 threads");
+    constexpr int kRegF4 = kRegElems / 4 / NTH;  // float4 per thread on the register path
+    constexpr int GRP = NTH / kThreads;          // threads per bound group (one key per group)
+    static_assert(GRP == 1 || GRP == 2 || GRP == 4, "bound group size");
     __shared__ uint32_t hist[256];
     __shared__ uint32_t sh_prefix, sh_remaining, sh_gt, sh_eq;
     __shared__ float cand_val[kMaxTopK];
     __shared__ int cand_idx[kMaxTopK];
-    __shared__ float red_val[kThreads / 64];
-    __shared__ int red_idx[kThreads / 64];
+    __shared__ float red_val[NTH / 64];
+    __shared__ int red_idx[NTH / 64];
     __shared__ uint32_t sh_thresh, sh_n;
     __shared__ __attribute__((aligned(16))) uint32_t tkey[kThreads];
     __shared__ uint32_t pool_key[kPoolCap];
@@ -119,20 +125,20 @@ __global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *lo
 #pragma unroll
         for (int j = 0; j < kRegF4; ++j)
             vals[j] = __builtin_bit_cast(
-                float4, __builtin_amdgcn_raw_buffer_load_b128(rr, (uint32_t)(tid + j * kThreads) * 16u, 0, 0));
+                float4, __builtin_amdgcn_raw_buffer_load_b128(rr, (uint32_t)(tid + j * NTH) * 16u, 0, 0));
     }
     auto visit = [&](auto &&fn) {
         if constexpr (REG) {
 #pragma unroll
             for (int j = 0; j < kRegF4; ++j) {
-                const int i0 = 4 * (tid + j * kThreads);
+                const int i0 = 4 * (tid + j * NTH);
                 if (i0 < V) fn(i0, vals[j].x);
                 if (i0 + 1 < V) fn(i0 + 1, vals[j].y);
                 if (i0 + 2 < V) fn(i0 + 2, vals[j].z);
                 if (i0 + 3 < V) fn(i0 + 3, vals[j].w);
             }
         } else {
-            for (int i = tid; i < V; i += kThreads) fn(i, row[i]);
+            for (int i = tid; i < V; i += NTH) fn(i, row[i]);
         }
     };
 
@@ -151,7 +157,7 @@ __global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *lo
         if (lane == 0) { red_val[wave] = best; red_idx[wave] = bi; }
         __syncthreads();
         if (tid == 0) {
-            for (int w = 1; w < kThreads / 64; ++w)
+            for (int w = 1; w < NTH / 64; ++w)
                 if (red_val[w] > best || (red_val[w] == best && red_idx[w] < bi)) { best = red_val[w]; bi = red_idx[w]; }
             tokens[s] = bi < V ? bi : 0;
         }
@@ -159,13 +165,20 @@ __global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *lo
     }
 
     const int k = top_k < V ? top_k : V;
-    // Lower bound: the k-th largest per-thread maximum (rank by key, then thread).
+    // Lower bound: the k-th largest of the 256 group maxima (a group is GRP
+    // adjacent threads; rank by key, then group): k groups hold a logit at
+    // least that large.
     uint32_t mk = 0;
     visit([&](int, float x) { mk = max(mk, order_key(x)); });
-    tkey[tid] = mk;
+    if constexpr (GRP >= 2)
+        mk = max(mk, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mk, dpp::kQuadXor1, 0xF, 0xF, false));
+    if constexpr (GRP >= 4)
+        mk = max(mk, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)mk, dpp::kQuadXor2, 0xF, 0xF, false));
+    if (tid % GRP == 0) tkey[tid / GRP] = mk;
     if (tid == 0) sh_n = 0;
     __syncthreads();
-    {
+    if (tid < kThreads) {
+        mk = tkey[tid];
         uint32_t rank = 0;
         const uint4 *t4 = reinterpret_cast<const uint4 *>(tkey);
 #pragma unroll 8
@@ -196,7 +209,7 @@ __global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *lo
     if (n_pool <= (uint32_t)kPoolCap) {
         // Exact rank of each pooled logit; ranks below k are the top k (the pool
         // order does not matter: a rank depends only on (key, token id)).
-        for (uint32_t c = tid; c < n_pool; c += kThreads) {
+        for (uint32_t c = tid; c < n_pool; c += NTH) {
             const uint32_t key = pool_key[c];
             const int idx = pool_idx[c];
             uint32_t rank = 0;
@@ -211,7 +224,7 @@ __global__ void __launch_bounds__(kThreads) sample_kernel(int V, const float *lo
             }
         }
     } else {
-        radix_topk(row, V, k, tid, hist, sh_prefix, sh_remaining, sh_gt, sh_eq, cand_val, cand_idx);
+        radix_topk<NTH>(row, V, k, tid, hist, sh_prefix, sh_remaining, sh_gt, sh_eq, cand_val, cand_idx);
     }
     __syncthreads();
     if (wave == 0) {
@@ -237,12 +250,12 @@ hipError_t launch_sample(int n, int V, const float *logits, float temperature, i
                          uint64_t counter, int32_t *tokens, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     if (temperature > 0.0f && (top_k < 1 || top_k > kMaxTopK)) return hipErrorInvalidValue;
-    if (V <= kThreads * 4 * kRegF4)
-        hipLaunchKernelGGL(sample_kernel<true>, dim3(n), dim3(kThreads), 0, stream, V, logits, temperature, top_k, seed,
-                           counter, tokens);
+    if (V <= kRegElems)
+        hipLaunchKernelGGL((sample_kernel<kRegThreads, true>), dim3(n), dim3(kRegThreads), 0, stream, V, logits,
+                           temperature, top_k, seed, counter, tokens);
     else
-        hipLaunchKernelGGL(sample_kernel<false>, dim3(n), dim3(kThreads), 0, stream, V, logits, temperature, top_k,
-                           seed, counter, tokens);
+        hipLaunchKernelGGL((sample_kernel<kThreads, false>), dim3(n), dim3(kThreads), 0, stream, V, logits,
+                           temperature, top_k, seed, counter, tokens);
     return hipGetLastError();
 }
 
