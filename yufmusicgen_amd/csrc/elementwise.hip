@@ -122,6 +122,97 @@ __global__ void embed_kernel(const int *tokens, int M, const float *table, int d
     for (int c = threadIdx.x; c < d; c += blockDim.x) dst[c] = ok ? src[c] : 0.0f;
 }
 
+// Prefill (T > 1) fusion of layernorm_kernel -> token_shift_kernel: each wave
+// walks a run of R consecutive tokens of one sequence, normalizing every row
+// with layernorm_kernel's expressions and reduction order (same bits) and
+// mixing it against the previous normed row it still holds in registers (the
+// run's first row against prev_state[slot[b]] at t = 0, else against its
+// recomputed predecessor); the normed rows never go to memory.  The wave whose
+// run ends the sequence writes that row to last_xn[b] for save_prev, which
+// runs afterwards (no wave overwrites prev_state while another may read it).
+template <int PER>
+__global__ void __launch_bounds__(256) ln_shift_seq_kernel(const float *__restrict__ x, int Bn, int T, int d, int R,
+                                                           const float *__restrict__ gamma,
+                                                           const float *__restrict__ beta,
+                                                           const float *__restrict__ prev_state,
+                                                           const int *__restrict__ slot,
+                                                           const float *__restrict__ mix6, float *__restrict__ out6,
+                                                           size_t out_stride, float *__restrict__ last_xn) {
+    const int runs = (T + R - 1) / R;
+    const int gw = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (gw >= Bn * runs) return;  // uniform over the wave; no barriers below
+    const int b = gw / runs, t0 = (gw - b * runs) * R, t1 = min(T, t0 + R);
+    float gm[PER], bt[PER], mx[6][PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = lane + e * kWave;
+        const bool ok = c < d;
+        gm[e] = ok ? gamma[c] : 0.0f;
+        bt[e] = ok ? beta[c] : 0.0f;
+#pragma unroll
+        for (int q = 0; q < 6; ++q) mx[q][e] = ok ? mix6[q * d + c] : 0.0f;
+    }
+    auto load_row = [&](int t, float (&v)[PER]) {
+        const float *xr = x + ((size_t)b * T + t) * d;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int c = lane + e * kWave;
+            v[e] = c < d ? xr[c] : 0.0f;
+        }
+    };
+    auto norm = [&](float (&v)[PER]) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) sum += v[e];
+        const float mean = wave_sum(sum) / (float)d;
+        float sq = 0.0f;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const float dv = lane + e * kWave < d ? v[e] - mean : 0.0f;
+            sq = fmaf(dv, dv, sq);
+        }
+        const float rstd = rsqrtf(wave_sum(sq) / (float)d + 1e-5f);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) v[e] = (v[e] - mean) * rstd * gm[e] + bt[e];
+    };
+    float pv[PER], cur[PER], nxt[PER] = {};
+    if (t0 == 0) {
+        const float *prow = prev_state + (size_t)(slot ? slot[b] : b) * d;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int c = lane + e * kWave;
+            pv[e] = c < d ? prow[c] : 0.0f;
+        }
+    } else {
+        load_row(t0 - 1, pv);
+        norm(pv);
+    }
+    load_row(t0, cur);
+    for (int t = t0; t < t1; ++t) {
+        if (t + 1 < t1) load_row(t + 1, nxt);
+        norm(cur);
+        float *orow = out6 + ((size_t)b * T + t) * d;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int c = lane + e * kWave;
+            if (c < d) {
+                const float delta = cur[e] - pv[e];
+#pragma unroll
+                for (int q = 0; q < 6; ++q) orow[q * out_stride + c] = fmaf(delta, mx[q][e], cur[e]);
+            }
+            pv[e] = cur[e];
+            cur[e] = nxt[e];
+        }
+    }
+    if (t1 == T) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int c = lane + e * kWave;
+            if (c < d) last_xn[(size_t)b * d + c] = pv[e];
+        }
+    }
+}
+
 __global__ void token_shift_kernel(const float *x, int Bn, int T, int d, const float *prev_state, const int *slot,
                                    const float *mix6, float *out6, size_t out_stride) {
     const size_t total = (size_t)Bn * T * d;
@@ -213,6 +304,30 @@ hipError_t launch_embed(const int *tokens, int M, const float *table, int d, int
                         hipStream_t stream) {
     if (M <= 0) return hipSuccess;
     hipLaunchKernelGGL(embed_kernel, dim3(M), dim3(256), 0, stream, tokens, M, table, d, vocab, out, bad);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_shift_seq(const float *x, int Bn, int T, int d, const float *gamma, const float *beta,
+                               const float *prev_state, const int *slot, const float *mix6, float *out6,
+                               size_t out_stride, float *last_xn, hipStream_t stream) {
+    if (Bn <= 0 || T <= 0) return hipSuccess;
+    constexpr int R = 16;  // tokens per wave: one extra LayerNorm per 16 rows
+    const int waves = Bn * ((T + R - 1) / R), per = (d + kWave - 1) / kWave;
+    const dim3 grid((waves + 3) / 4), block(256);
+    if (per <= 2)
+        hipLaunchKernelGGL(ln_shift_seq_kernel<2>, grid, block, 0, stream, x, Bn, T, d, R, gamma, beta, prev_state, slot,
+                           mix6, out6, out_stride, last_xn);
+    else if (per <= 4)
+        hipLaunchKernelGGL(ln_shift_seq_kernel<4>, grid, block, 0, stream, x, Bn, T, d, R, gamma, beta, prev_state, slot,
+                           mix6, out6, out_stride, last_xn);
+    else if (per <= 10)
+        hipLaunchKernelGGL(ln_shift_seq_kernel<10>, grid, block, 0, stream, x, Bn, T, d, R, gamma, beta, prev_state,
+                           slot, mix6, out6, out_stride, last_xn);
+    else if (per <= 16)
+        hipLaunchKernelGGL(ln_shift_seq_kernel<16>, grid, block, 0, stream, x, Bn, T, d, R, gamma, beta, prev_state,
+                           slot, mix6, out6, out_stride, last_xn);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

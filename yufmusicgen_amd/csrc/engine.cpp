@@ -398,6 +398,12 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         if (Tc == 1 && d <= 1024) {
             ENG_TRY(launch_ln_shift(a.h, n, d, w.ln_t_w, w.ln_t_b, prev, a.slots, w.mix6, a.mix, plane, st),
                     "ln_shift");
+        } else if (d <= 1024) {
+            // LayerNorm + token shift in one pass; the last normed row of each
+            // stream goes through a.hl (free until the LM head) to prev.
+            ENG_TRY(launch_ln_shift_seq(a.h, n, Tc, d, w.ln_t_w, w.ln_t_b, prev, a.slots, w.mix6, a.mix, plane, a.hl,
+                                        st), "ln_shift_seq");
+            ENG_TRY(launch_save_prev(a.hl, n, 1, d, prev, a.slots, st), "save_prev");
         } else {
             ENG_TRY(launch_layernorm(a.h, M, d, w.ln_t_w, w.ln_t_b, nullptr, a.xn, st), "ln_time");
             ENG_TRY(launch_token_shift(a.xn, n, Tc, d, prev, a.slots, w.mix6, a.mix, plane, st), "token_shift");

@@ -159,6 +159,12 @@ hipError_t launch_token_shift(const float *x, int Bn, int T, int d, const float 
 // rows and prev_state[slot[b]] <- LayerNorm(x[b]); d <= 1024.
 hipError_t launch_ln_shift(const float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
                            const int *slot, const float *mix6, float *out6, size_t out_stride, hipStream_t stream);
+// T > 1 fusion of layernorm -> token_shift: out6 from the normed rows (the
+// normed rows themselves are not stored) and last_xn[b] <- the normed row
+// t = T - 1 (for launch_save_prev with T = 1 afterwards); d <= 1024.
+hipError_t launch_ln_shift_seq(const float *x, int Bn, int T, int d, const float *gamma, const float *beta,
+                               const float *prev_state, const int *slot, const float *mix6, float *out6,
+                               size_t out_stride, float *last_xn, hipStream_t stream);
 // prev_state[slot[b]] = x[b, T - 1, :]
 hipError_t launch_save_prev(const float *x, int Bn, int T, int d, float *prev_state, const int *slot,
                             hipStream_t stream);
