@@ -280,6 +280,7 @@ hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, co
     if (per <= 2) hipLaunchKernelGGL(layernorm_kernel<2>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
     else if (per <= 4) hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
     else if (per <= 8) hipLaunchKernelGGL(layernorm_kernel<8>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
+    else if (per <= 10) hipLaunchKernelGGL(layernorm_kernel<10>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
     else if (per <= 16) hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
     else if (per <= kMaxPerLane)
         hipLaunchKernelGGL(layernorm_kernel<kMaxPerLane>, grid, block, 0, stream, x, M, d, gamma, beta, gate, out);
