@@ -597,18 +597,22 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
     if (!(e.step_exec[0] && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
         int rc = drop_step_graphs(e);
         if (rc != YUF_OK) return rc;
+        // The graphs read the caller's token ids in place (a graph is re-captured
+        // when that pointer changes), so a replay needs no copy node.
         if (G == 1) {
             rc = capture(e.stream, [&]() {
-                ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice,
-                                       e.stream), "tokens copy");
-                return forward_pass(e, act_at(e, e.stream, 0, 1), n, 1, logits_dev, YUF_LOGITS_LAST, 1, 0);
+                Act a = act_at(e, e.stream, 0, 1);
+                a.tokens = tokens_dev;
+                return forward_pass(e, a, n, 1, logits_dev, YUF_LOGITS_LAST, 1, 0);
             }, &e.step_exec[0]);
         } else {
             for (int g = 0; g < G && rc == YUF_OK; ++g) {
                 const auto [s0, s1] = group(g);
                 hipStream_t st = stream_of(g);
                 rc = capture(st, [&]() {
-                    return forward_pass(e, act_at(e, st, s0, 1), s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
+                    Act a = act_at(e, st, s0, 1);
+                    a.tokens = tokens_dev + s0;
+                    return forward_pass(e, a, s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
                 }, &e.step_exec[g]);
             }
             if (rc == YUF_OK)
@@ -627,8 +631,6 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
         ENG_TRY(hipGraphLaunch(e.step_exec[0], e.stream), "graph launch");
         return YUF_OK;
     }
-    ENG_TRY(hipMemcpyAsync(e.tokens_dev, tokens_dev, (size_t)n * sizeof(int), hipMemcpyDeviceToDevice, e.stream),
-            "tokens copy");
     ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
     for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.side[g - 1], e.fork, 0), "fork wait");
     for (int g = 0; g < G; ++g) ENG_TRY(hipGraphLaunch(e.step_exec[g], stream_of(g)), "graph launch");
