@@ -59,15 +59,19 @@ __global__ void __launch_bounds__(256) layernorm_kernel(const float *x, int M, i
 // workgroup per row.  Every load (row, previous row, affine, mixes) is issued
 // before the first store, so the kernel costs one memory round trip; each
 // thread reads a column's previous value before it overwrites it.
+constexpr int kMaxParts = 4;  // K-split partial planes ln_shift_kernel can add
+
 template <int PER>
-__global__ void __launch_bounds__(256) ln_shift_kernel(const float *__restrict__ x, int d,
+__global__ void __launch_bounds__(256) ln_shift_kernel(float *__restrict__ x, int d,
                                                        const float *__restrict__ gamma,
                                                        const float *__restrict__ beta, float *__restrict__ prev_state,
                                                        const int *__restrict__ slot, const float *__restrict__ mix6,
-                                                       float *__restrict__ out6, size_t out_stride) {
+                                                       float *__restrict__ out6, size_t out_stride,
+                                                       const float *__restrict__ parts, size_t part_stride,
+                                                       int nparts) {
     __shared__ float part[2][4];
     const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const float *xr = x + (size_t)row * d;
+    float *xr = x + (size_t)row * d;
     float *prow = prev_state + (size_t)(slot ? slot[row] : row) * d;
     float v[PER], pv[PER], gm[PER], bt[PER], mx[6][PER];
     float sum = 0.0f;
@@ -81,6 +85,30 @@ __global__ void __launch_bounds__(256) ln_shift_kernel(const float *__restrict__
         bt[e] = ok ? beta[c] : 0.0f;
 #pragma unroll
         for (int q = 0; q < 6; ++q) mx[q][e] = ok ? mix6[q * d + c] : 0.0f;
+    }
+    // Pending K-split partial sums of the previous product (h += P0 + P1 + ...,
+    // in order): loaded with the row (unused parts read as zero outside the
+    // descriptor), the row is completed and written back before it is normed.
+    float pp[kMaxParts][PER];
+    const auto rpart = make_rsrc(parts ? parts + (size_t)row * d : nullptr,
+                                 parts ? (uint32_t)(((size_t)(kMaxParts - 1) * part_stride + d) * 4) : 0u);
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int c = tid + e * 256;
+            pp[q][e] = buf_load(rpart, q < nparts && c < d ? (uint32_t)((size_t)q * part_stride + c) * 4u : kBufferOob);
+        }
+#pragma unroll
+    for (int q = 0; q < kMaxParts; ++q)
+        if (q < nparts) {
+#pragma unroll
+            for (int e = 0; e < PER; ++e) v[e] += pp[q][e];
+        }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int c = tid + e * 256;
+        if (nparts > 0 && c < d) xr[c] = v[e];
         sum += v[e];
     }
     sum = wave_sum(sum);
@@ -288,16 +316,35 @@ hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, co
     return hipGetLastError();
 }
 
-hipError_t launch_ln_shift(const float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
-                           const int *slot, const float *mix6, float *out6, size_t out_stride, hipStream_t stream) {
+hipError_t launch_ln_shift(float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
+                           const int *slot, const float *mix6, float *out6, size_t out_stride, const float *parts,
+                           size_t part_stride, int nparts, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
+    if (nparts < 0 || nparts > kMaxParts || (nparts > 0 && !parts)) return hipErrorInvalidValue;
     const dim3 grid(n), block(256);
     const int per = (d + 255) / 256;
-    if (per <= 1) hipLaunchKernelGGL(ln_shift_kernel<1>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
-    else if (per <= 2) hipLaunchKernelGGL(ln_shift_kernel<2>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
-    else if (per <= 3) hipLaunchKernelGGL(ln_shift_kernel<3>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
-    else if (per <= 4) hipLaunchKernelGGL(ln_shift_kernel<4>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride);
+    if (per <= 1) hipLaunchKernelGGL(ln_shift_kernel<1>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
+    else if (per <= 2) hipLaunchKernelGGL(ln_shift_kernel<2>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
+    else if (per <= 3) hipLaunchKernelGGL(ln_shift_kernel<3>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
+    else if (per <= 4) hipLaunchKernelGGL(ln_shift_kernel<4>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
     else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// x[m, c] += parts[0][m, c] + parts[1][m, c] + ... (in order), rows of width d.
+__global__ void add_parts_kernel(float *x, size_t n, const float *parts, size_t part_stride, int nparts) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float v = x[i];
+        for (int q = 0; q < nparts; ++q) v += parts[q * part_stride + i];
+        x[i] = v;
+    }
+}
+
+hipError_t launch_add_parts(float *x, int M, int d, const float *parts, size_t part_stride, int nparts,
+                            hipStream_t stream) {
+    const size_t n = (size_t)M * d;
+    if (n == 0 || nparts <= 0) return hipSuccess;
+    hipLaunchKernelGGL(add_parts_kernel, dim3(grid_for(n, 256)), dim3(256), 0, stream, x, n, parts, part_stride, nparts);
     return hipGetLastError();
 }
 

@@ -48,6 +48,7 @@ struct LayerW {
 
 // Segment length of the segmented ROSA prefill scan.
 constexpr int kRosaSeg = 64;
+constexpr int kFfnParts = 4;  // K split of the decode FFN output product (partials summed by their consumer)
 
 struct DeviceBuf {
     void *p = nullptr;
@@ -77,6 +78,7 @@ struct Engine {
           *al = nullptr, *g = nullptr, *lr = nullptr, *y = nullptr, *z = nullptr, *rosa3 = nullptr, *rread = nullptr,
           *ffn = nullptr, *hl = nullptr;
     float *rz = nullptr, *rcarry = nullptr, *rends = nullptr;  // segmented ROSA scratch
+    float *kpart = nullptr;  // [kFfnParts][max_streams][d]: K-split partials of the decode FFN output
     bool rosa_segmented = true;                                // YUF_ROSA_SEGMENTED=0 disables
     bool decode_fusion = true;                                 // YUF_DECODE_FUSION=0: separate low-rank GEMM and ROSA step
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
@@ -347,6 +349,8 @@ struct Act {
     float *rz, *rcarry, *rends;  // segmented ROSA scratch (segment rows of kRosaSeg tokens)
     const int *tokens, *slots;
     int *rcount;  // fused ROSA-out tile counters of this group of streams
+    float *kpart;  // FFN-out K-split partials of these streams, planes kplane floats apart
+    size_t kplane;
 };
 
 Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
@@ -366,6 +370,8 @@ Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
     a.tokens = e.tokens_dev + m0;
     a.slots = e.slots_dev + s0;
     a.rcount = e.rosa_count + s0;
+    a.kpart = e.kpart + (size_t)s0 * d;
+    a.kplane = (size_t)e.max_streams * d;
     return a;
 }
 
@@ -389,6 +395,10 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     const size_t plane = (size_t)e.max_tokens * d, lplane = (size_t)e.max_tokens * L;
     hipStream_t st = a.st;
     ENG_TRY(launch_embed(a.tokens, M, e.emb, d, V, a.h, e.bad_dev, st), "embed");
+    // Decode: the FFN output product is split over K into kFfnParts products
+    // (four times the workgroups); the partial sums stay in a.kpart until the
+    // next layer's ln_shift (or, after the last layer, add_parts) adds them to h.
+    const bool ffn_split = Tc == 1 && e.decode_fusion && !e.w_h && M <= 64 && d <= 1024 && hid % (16 * kFfnParts) == 0;
     for (int l = 0; l < s.layers; ++l) {
         const LayerW &w = e.layers[l];
         float *prev = e.st_prev + (size_t)l * e.max_streams * d;
@@ -396,8 +406,10 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         float *ros = e.st_rosa + (size_t)l * e.max_streams * D;
         // TimeMix
         if (Tc == 1 && d <= 1024) {
-            ENG_TRY(launch_ln_shift(a.h, n, d, w.ln_t_w, w.ln_t_b, prev, a.slots, w.mix6, a.mix, plane, st),
-                    "ln_shift");
+            // The previous layer's FFN output may be pending as K-split partials.
+            const int np = ffn_split && l > 0 ? kFfnParts : 0;
+            ENG_TRY(launch_ln_shift(a.h, n, d, w.ln_t_w, w.ln_t_b, prev, a.slots, w.mix6, a.mix, plane,
+                                    np ? a.kpart : nullptr, a.kplane, np, st), "ln_shift");
         } else if (d <= 1024) {
             // LayerNorm + token shift in one pass; the last normed row of each
             // stream goes through a.hl (free until the LM head) to prev.
@@ -490,9 +502,20 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         if ((rc = ln_gemm(e, st, M, 2 * hid, d, a.h, d, w.ln_f_w, w.ln_f_b, nullptr, a.xn, w.ffn_cat, a.ffn, hid,
                           nullptr, nullptr, 0, true)) != YUF_OK)
             return rc;
-        if ((rc = gemm(e, st, M, d, hid, a.ffn, hid, w.ffn_out, hid, a.h, d, nullptr, ACT_NONE, a.h, d)) != YUF_OK)
+        if (ffn_split) {
+            const int kp = hid / kFfnParts;
+            GemmParams parts[kFfnParts];
+            for (int q = 0; q < kFfnParts; ++q)
+                parts[q] = make_gemm(e, M, d, kp, a.ffn + (size_t)q * kp, hid, w.ffn_out + (size_t)q * kp, hid,
+                                     a.kpart + (size_t)q * a.kplane, d);
+            if ((rc = gemm_group(st, parts, kFfnParts)) != YUF_OK) return rc;
+        } else if ((rc = gemm(e, st, M, d, hid, a.ffn, hid, w.ffn_out, hid, a.h, d, nullptr, ACT_NONE, a.h, d)) !=
+                   YUF_OK) {
             return rc;
+        }
     }
+    if (ffn_split && s.layers > 0)
+        ENG_TRY(launch_add_parts(a.h, M, d, a.kpart, a.kplane, kFfnParts, st), "ffn partials");
     if (mode == YUF_LOGITS_LAST) return lm_head_last(e, a, n, Tc, logits);
     if (mode == YUF_LOGITS_ALL) {
         ENG_TRY(launch_layernorm(a.h, M, d, e.ln_fin_w, e.ln_fin_b, nullptr, a.xn, st), "ln_final");
@@ -784,14 +807,14 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     const size_t sizes[] = {Mx * d, Mx * d, 6 * Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d,
                             3 * Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
                             (size_t)max_streams * d, ws, Mx / kRosaSeg * s.rosa + s.rosa, Mx / kRosaSeg * s.rosa + s.rosa,
-                            Mx / kRosaSeg * s.rosa + s.rosa};
+                            Mx / kRosaSeg * s.rosa + s.rosa, (size_t)kFfnParts * max_streams * d};
     size_t total = 0;
     for (size_t z : sizes) total += ((z * sizeof(float) + 255) / 256) * 256;
     ENG_TRY(hipMalloc(&e.work.p, total), "workspace alloc");
     {
         char *cur = static_cast<char *>(e.work.p);
         float **dst[] = {&e.h, &e.xn, &e.mix, &e.r, &e.k, &e.v, &e.wr, &e.al, &e.g, &e.lr, &e.y, &e.z, &e.rosa3,
-                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.rends};
+                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.rends, &e.kpart};
         for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
     }
     const size_t io_bytes = 256 * 4 + (size_t)(2 * max_streams + max_tokens + 1) * sizeof(int);

@@ -157,8 +157,14 @@ hipError_t launch_token_shift(const float *x, int Bn, int T, int d, const float 
                               hipStream_t stream);
 // T = 1 fusion of layernorm -> token_shift -> save_prev: out6 from the normed
 // rows and prev_state[slot[b]] <- LayerNorm(x[b]); d <= 1024.
-hipError_t launch_ln_shift(const float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
-                           const int *slot, const float *mix6, float *out6, size_t out_stride, hipStream_t stream);
+// nparts > 0: x[b] += parts[0][b] + parts[1][b] + ... (part planes part_stride
+// floats apart, rows of width d) first, and the completed row is written back.
+hipError_t launch_ln_shift(float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
+                           const int *slot, const float *mix6, float *out6, size_t out_stride, const float *parts,
+                           size_t part_stride, int nparts, hipStream_t stream);
+// x[m] += parts[0][m] + parts[1][m] + ... in order (M rows of width d).
+hipError_t launch_add_parts(float *x, int M, int d, const float *parts, size_t part_stride, int nparts,
+                            hipStream_t stream);
 // T > 1 fusion of layernorm -> token_shift: out6 from the normed rows (the
 // normed rows themselves are not stored) and last_xn[b] <- the normed row
 // t = T - 1 (for launch_save_prev with T = 1 afterwards); d <= 1024.
