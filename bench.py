@@ -25,10 +25,13 @@ In the same run:
 
 Only N = 1 GPU exists on these boxes; --gpus above 1 exits with a message.
 
-`--only c5` (not part of the default run): the C5 architecture (24 layers,
-d_model 1024, 16 x 64 heads, ROSA 256) with fp32 and with bf16 projection
-weights on a bounded slice of C5 (32 rows x 1024 tokens of prefill, last-position
-logits, then 64 decode steps of the 32 streams).
+`--only c5` (not part of the default run): C5 as configured -- the wide model
+(24 layers, d_model 1024, 16 x 64 heads, ROSA 256) with bf16 projection weights,
+B = 32 x T = 8192 tokens of prefill (last-position logits), then 512 decode
+steps of the 32 streams -- and the same workload with fp32 weights.
+
+`cpu_baseline_decode` / `cpu_baseline_scan`: the oracle's float32 single-token
+step of C4 (64 streams) and its sequential C2 scan, on the same host cores.
 """
 
 from __future__ import annotations
@@ -171,55 +174,76 @@ def bench_gemm(iters: int) -> dict:
 
 
 def bench_c5(args) -> dict:
-    """C5 architecture, fp32 vs bf16 projection weights, bounded slice."""
+    """C5 as configured: the wide model (24 layers,
+    d_model 1024, 16 x 64 heads, ROSA 256, V 20480) with bf16 projection weights
+    and fp32 WKV / ROSA state; B = 32 rows x T = 8192 tokens of prefill
+    (T-chunked through a 32 x 2048-token engine pass, the state carried,
+    last-position logits), then 512 decode steps of the 32 streams with device
+    top-k = 32, T = 1.0 sampling.  The fp32-weight engine runs the same workload
+    once for comparison."""
     import torch
 
     from yufmusicgen_amd.checkpoint import write_yuf
     from yufmusicgen_amd.config import PRESETS
-    from yufmusicgen_amd.engine import Checkpoint, Engine
-    from yufmusicgen_amd.synth import prompt_tokens, synth_weights, uniform_tokens
+    from yufmusicgen_amd.engine import Checkpoint, Engine, sample_device
+    from yufmusicgen_amd.synth import prompt_tokens, synth_weights
 
     cfg = PRESETS["wide"]
     log("c5: generating weights")
     weights = synth_weights(cfg, seed=0)
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "c5.yuf")
-        write_yuf(path, cfg, weights)
+        write_yuf(path, cfg, weights, linear_bf16=True)
         ckpt = Checkpoint.load(path)
-    B, T, D = 32, 1024, 64
+    del weights
+    B, T, D, chunk = 32, 8192, args.c5_decode_steps, 2048
     tokens = torch.from_numpy(prompt_tokens(0, B, T, cfg.vocab_size)).cuda()
-    step_tokens = torch.from_numpy(uniform_tokens(1, B, D, cfg.vocab_size)).cuda()
     slots = np.arange(B, dtype=np.int32)
-    out = {"workload": f"C5 architecture (24L, d=1024, 16x64, ROSA 256), prefill {B}x{T} last logits, "
-                       f"then {D} decode steps of {B} streams"}
-    for wt in ("f32", "bf16"):
-        engine = Engine(ckpt, max_streams=B, max_tokens=B * T, weight_dtype=wt)
+    out = {"workload": f"C5: 24L d=1024 16x64 ROSA 256 V=20480, bf16 weights (.yuf v2), prefill {B}x{T} "
+                       f"(T-chunks of {chunk}, last logits), then {D} decode steps of {B} streams "
+                       "(device top-k=32 T=1.0 sampling)"}
+    for wt, reps in (("bf16", max(1, args.c5_steps)), ("f32", 1)):
+        engine = Engine(ckpt, max_streams=B, max_tokens=B * chunk, weight_dtype=wt)
+        stream = torch.cuda.ExternalStream(engine.stream)
         logits = torch.empty(B, cfg.vocab_size, device="cuda")
-        for _ in range(max(1, args.warmup)):
+        step_tok = torch.empty(B, dtype=torch.int32, device="cuda")  # one buffer: the step graph reads it in place
+        engine.reset_state()
+        engine.prefill_device(tokens, logits, slots, logits="last")  # warm-up (capture, first touches)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
             engine.reset_state()
             engine.prefill_device(tokens, logits, slots, logits="last")
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            engine.reset_state()
-            engine.prefill_device(tokens, logits, slots, logits="last")
-        torch.cuda.synchronize()
-        pf = (time.perf_counter() - t0) / args.steps
-        for t in range(3):
-            engine.step_device(step_tokens[:, t].contiguous(), logits, slots)
+        pf = (time.perf_counter() - t0) / reps
+        with torch.cuda.stream(stream):
+            sample_device(logits, step_tok, 1.0, 32, seed=99, counter=0, stream=engine.stream)
+        for i in range(3):  # warm-up steps (graph capture)
+            engine.step_device(step_tok, logits, slots)
+            sample_device(logits, step_tok, 1.0, 32, seed=99, counter=1 + i, stream=engine.stream)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for t in range(D):
-            engine.step_device(step_tokens[:, t].contiguous(), logits, slots)
+        for i in range(D):
+            engine.step_device(step_tok, logits, slots)
+            sample_device(logits, step_tok, 1.0, 32, seed=99, counter=100 + i, stream=engine.stream)
         torch.cuda.synchronize()
         dc = (time.perf_counter() - t0) / D
+        engine.take_error()
         out[wt] = {"prefill_tokens_per_s": round(B * T / pf), "prefill_ms": round(pf * 1e3, 2),
-                   "decode_tokens_per_s": round(B / dc), "decode_ms_per_step": round(dc * 1e3, 3)}
+                   "decode_tokens_per_s": round(B / dc), "decode_ms_per_step": round(dc * 1e3, 3),
+                   "prefill_reps": reps}
         log(f"c5 {wt}: prefill {pf * 1e3:.1f} ms ({B * T / pf:.0f} tok/s), decode {dc * 1e3:.3f} ms/step")
         engine.close()
         del engine
         torch.cuda.empty_cache()
     return out
+
+
+def _cpu_threads() -> int:
+    import torch
+
+    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
+    return torch.get_num_threads()
 
 
 def cpu_baseline(weights, cfg) -> dict:
@@ -228,8 +252,7 @@ def cpu_baseline(weights, cfg) -> dict:
     from oracle.model import OracleModel
     from yufmusicgen_amd.synth import prompt_tokens
 
-    torch.set_num_threads(max(1, len(os.sched_getaffinity(0))))
-    cores = torch.get_num_threads()
+    cores = _cpu_threads()
     B, T = 8, 1024
     tokens = prompt_tokens(7, B, T, cfg.vocab_size)
     model = OracleModel(cfg.to_dict(), weights, dtype=torch.float32)
@@ -246,6 +269,60 @@ def cpu_baseline(weights, cfg) -> dict:
                       f"restatement of the reference fallback, median of 3 = {sec:.2f} s"}
 
 
+def cpu_baseline_decode(weights, cfg, steps: int = 8) -> dict:
+    """C4 decode on the host: the float32 oracle's single-token step
+    (model.py:424-431, the per-token path of cli/generate.py:139-154) for 64
+    streams from a 256-token prefilled state, median of `steps` steps."""
+    import torch
+
+    from oracle.model import OracleModel
+    from yufmusicgen_amd.synth import uniform_tokens
+
+    cores = _cpu_threads()
+    S, P = 64, 256
+    model = OracleModel(cfg.to_dict(), weights, dtype=torch.float32)
+    with torch.no_grad():
+        _, state = model.forward(uniform_tokens(3, S, P, cfg.vocab_size), logits="last")
+        nxt = uniform_tokens(4, S, steps + 1, cfg.vocab_size)
+        _, state = model.step(nxt[:, 0], state)  # warm-up
+        times = []
+        for t in range(1, steps + 1):
+            t0 = time.perf_counter()
+            _, state = model.step(nxt[:, t], state)
+            times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    return {"value": round(S / sec, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "ms_per_step": round(sec * 1e3, 2),
+            "sample": f"C4 decode: {steps} single-token steps of {S} streams after a {P}-token prefill (0.1B model), "
+                      f"fp32 torch CPU restatement of the reference's per-token path, median step {sec * 1e3:.1f} ms"}
+
+
+def cpu_baseline_scan() -> dict:
+    """C2 on the host: the float32 oracle's sequential WKV-7 scan
+    (model.py:145-165) at the full C2 shape, median of 3."""
+    import torch
+
+    from oracle import wkv7 as owkv
+    from yufmusicgen_amd.synth import wkv_inputs
+
+    cores = _cpu_threads()
+    B, T, H, N = 8, 2048, 16, 40
+    arrs = [torch.from_numpy(x) for x in wkv_inputs(0, B, T, H, N)]
+    with torch.no_grad():
+        owkv.wkv7_scan(*(x[:, :16] for x in arrs))  # warm-up
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            owkv.wkv7_scan(*arrs)
+            times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    nbytes = wkv_bytes(B, T, H, N)
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s (algorithmic)", "cores": cores, "kind": "port",
+            "us_per_scan": round(sec * 1e6, 1), "tokens_per_s": round(B * T / sec, 1),
+            "sample": f"C2 scan B={B} T={T} H={H} N={N}, zero state, fp32 torch CPU restatement of the "
+                      f"reference recurrence, median of 3 = {sec:.3f} s"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +330,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--c5-steps", type=int, default=2, help="timed C5 prefills (--only c5)")
+    ap.add_argument("--c5-decode-steps", type=int, default=512, help="C5 decode steps (--only c5)")
     ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5", "kernels", "gemm"], default=None,
                     help="profiling aids: just the C2 scan (20 launches), just the prefill steps, just the C4 "
                          "decode leg, a plain 256 MiB device copy (20 launches) that calibrates the "
@@ -369,11 +448,15 @@ def main() -> int:
     log(f"rosa {rosa['avg_us']} us, {rosa['achieved']} GB/s")
     gemm = bench_gemm(10)
     log(f"gemm {gemm['achieved']} TFLOP/s")
-    cpu = None
+    cpu = cpu_dec = cpu_scan = None
     if not args.no_cpu_baseline:
         log("cpu baseline")
         cpu = cpu_baseline(weights, cfg)
         log(f"cpu {cpu['value']} tokens/s on {cpu['cores']} cores")
+        cpu_dec = cpu_baseline_decode(weights, cfg)
+        log(f"cpu decode {cpu_dec['value']} tokens/s ({cpu_dec['ms_per_step']} ms/step)")
+        cpu_scan = cpu_baseline_scan()
+        log(f"cpu scan {cpu_scan['us_per_scan']} us ({cpu_scan['value']} GB/s)")
 
     out = {
         "metric": METRIC,
@@ -401,6 +484,8 @@ def main() -> int:
         "rosa_roofline": rosa,
         "gemm_roofline": gemm,
         "cpu_baseline": cpu,
+        "cpu_baseline_decode": cpu_dec,
+        "cpu_baseline_scan": cpu_scan,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -124,8 +124,10 @@ int yuf_ln_linear_f32(int M, int N, int K, const float *A, const float *gamma, c
  * bf16-weight forms of yuf_linear_f32 / yuf_ln_linear_f32 (the C5
  * configuration's weight type; no counterpart in the fp32 reference kernels,
  * they replace the same nn.Linear call sites).  W is [N, K] bf16 (raw 16-bit
- * patterns, uint16_t); A, bias, residual and C are fp32.  A is rounded to bf16
- * (nearest even) as it enters the matrix cores; accumulation is fp32.
+ * patterns, uint16_t); A, bias, residual and C are fp32.  The result is the
+ * fp32 product A x W up to accumulation order: each A value enters the bf16
+ * matrix cores as two bf16 parts (hi = bf16(a), lo = bf16(a - hi), within
+ * 2^-16 of a) and accumulation is fp32.
  * Needs K % 8 == 0; for M > 64, N % 64 == 0 or N % 160 == 0.
  */
 int yuf_linear_bf16w(int M, int N, int K, const float *A, const uint16_t *W,
@@ -157,11 +159,23 @@ typedef struct {
     int32_t midi_vocab_size;
 } yuf_model_config;
 
-/* Load and validate a .yuf file (magic "YUFM", version 1, JSON header,
- * f32 payload whose size must match; checkpoint.rs:90-149). */
+/* Load and validate a .yuf file (checkpoint.rs:90-149): magic "YUFM", a u32
+ * version, a u64 header length, the UTF-8 JSON header, then the payload.
+ * Version 1 is the reference's format (f32 payload whose size must equal
+ * 4 * sum(count)); version 2 is this library's extension for bf16 weights
+ * (per-tensor "dtype" and byte "offset", a "payload_bytes" the file size must
+ * match; bf16 tensors are widened to f32 on load). */
 int yuf_ckpt_load(const char *path, yuf_ckpt **out);
 void yuf_ckpt_free(yuf_ckpt *ckpt);
 int yuf_ckpt_config(const yuf_ckpt *ckpt, yuf_model_config *out);
+/* The file's JSON header, verbatim (NUL-terminated; *len bytes without the
+ * NUL), and its container version.  Replaces the reference's parsed
+ * `checkpoint.header` (checkpoint.rs:60-81: format, model_config, midi{
+ * tokenization, midi_offset, midi_vocab_size, vocab[], tokenizer_json},
+ * source, lm_head_alias, tensors[]), which its generation loop reads to build
+ * the codec and check the vocabulary (vulkan/src/generation.rs:102-117).
+ * The pointer stays valid until yuf_ckpt_free.  len / version may be NULL. */
+int yuf_ckpt_header_json(const yuf_ckpt *ckpt, const char **json, size_t *len, uint32_t *version);
 /* Borrow a tensor by name (checkpoint.rs:151-176): host pointer valid until
  * yuf_ckpt_free; dims receives up to 8 sizes. */
 int yuf_ckpt_tensor(const yuf_ckpt *ckpt, const char *name, const float **data,
@@ -188,12 +202,13 @@ enum { YUF_WEIGHTS_F32 = 0, YUF_WEIGHTS_BF16 = 1 };
 
 /* yuf_engine_create with a projection-weight type (the `weight_dtype`
  * argument of the engine API; the C5 configuration runs bf16 weights with
- * fp32 accumulation, yufmusicgen/config.py:73-93).  YUF_WEIGHTS_BF16 keeps a
- * bf16 copy (round to nearest even, or the file's own bf16 values) of every
- * nn.Linear weight and the tied LM head; the GEMMs round their fp32
- * activations to bf16 and accumulate in fp32.  Everything else (LayerNorm,
- * the WKV-7 and ROSA recurrences, state) stays fp32.  Needs d_model, the
- * low-rank width and rosa_size to be multiples of 8, and the prefill GEMM
+ * fp32 WKV / ROSA state, yufmusicgen/config.py:73-93).  YUF_WEIGHTS_BF16 keeps
+ * a bf16 copy (round to nearest even, or the file's own bf16 values) of every
+ * nn.Linear weight and the tied LM head and runs the projections on the bf16
+ * matrix cores with fp32-precision activations (see yuf_linear_bf16w): the
+ * result is the fp32 model on bf16-valued weights.  Everything else
+ * (LayerNorm, the WKV-7 and ROSA recurrences, state) is fp32.  Needs d_model,
+ * the low-rank width and rosa_size to be multiples of 8, and the prefill GEMM
  * widths (d, low rank, 3 rosa_size, vocab) multiples of 64 or 160. */
 int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int max_tokens, int weight_type,
                          yuf_engine **out);
@@ -214,7 +229,10 @@ int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T,
                 const int32_t *tokens, float *logits, int logits_mode);
 
 /* Same with device-resident tokens and logits, asynchronous on the engine's
- * stream (slots stay host).  Use for throughput measurements. */
+ * stream (slots stay host).  Use for throughput measurements.  Token ids are
+ * read on the device: an id outside [0, vocab) embeds as zeros and sets the
+ * engine's device-error flag, reported by yuf_engine_take_error (the host
+ * entry points validate ids on the host and keep a flag of their own). */
 int yuf_prefill_device(yuf_engine *eng, int n, const int32_t *slots, int T,
                        const int32_t *tokens_dev, float *logits_dev, int logits_mode);
 
@@ -222,9 +240,22 @@ int yuf_prefill_device(yuf_engine *eng, int n, const int32_t *slots, int T,
  * Model::step, model.rs:54-60).  Host buffers, synchronous. */
 int yuf_step(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens, float *logits);
 
-/* Same with device tokens / logits, asynchronous on the engine's stream. */
+/* Same with device tokens / logits, asynchronous on the engine's stream.
+ * The step is replayed from a captured HIP graph that reads tokens_dev and
+ * writes logits_dev in place; the graph is captured again whenever n,
+ * tokens_dev or logits_dev differ from the previous call, so a decode loop
+ * should reuse one token buffer and one logits buffer.  tokens_dev must hold
+ * its ids when the engine stream reaches the step (write it on that stream,
+ * or synchronise first).  Out-of-range ids: see yuf_prefill_device. */
 int yuf_step_device(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens_dev,
                     float *logits_dev);
+
+/* Synchronise the engine stream and report (then clear) the device-error flag
+ * of the device entry points: YUF_ERR_RANGE if a yuf_prefill_device /
+ * yuf_step_device call since the last check read a token id outside
+ * [0, vocab) (its embedding row was zeroed), else YUF_OK.  No counterpart in
+ * the reference, whose engine takes host token ids only (model.rs:54-60). */
+int yuf_engine_take_error(yuf_engine *eng);
 
 /* Zero all recurrent state of one slot (slot = -1: every slot), including
  * the token-shift `previous` vector the reference reset leaves stale

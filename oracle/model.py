@@ -14,12 +14,12 @@ Follows ``yufmusicgen/model.py`` op for op with ``use_cuda_kernel=False`` and
 Weights are a dict keyed by the reference's ``state_dict`` names (the names
 the ``.yuf`` container carries, ``vulkan/src/compute/model.rs:916-951``).
 
-``bf16_linear=True`` restates the bf16-weight configuration (C5's weight type,
-fp32 accumulation): every nn.Linear weight and the LM head (not the embedding
-gather) is rounded to bf16, and every projection input is rounded to bf16
-before its product; products accumulate in ``dtype``; everything else (norms,
-gates, both recurrences) is unchanged.  Rounding is torch's float32 ->
-bfloat16 cast (round to nearest even).
+``bf16_linear=True`` restates the bf16-weight configuration (C5's weight type):
+every nn.Linear weight and the LM head (not the embedding gather) is rounded to
+bf16 -- torch's float32 -> bfloat16 cast, round to nearest even -- and the model
+then computes in ``dtype`` as the fp32 reference does (projection inputs are
+not rounded; norms, gates and both recurrences are unchanged).  This is the
+reference PyTorch module loaded with bf16-valued weights.
 """
 
 from __future__ import annotations
@@ -95,7 +95,7 @@ class OracleModel:
 
     def _mm(self, x: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
         """x @ m for a projection (m already in its product orientation)."""
-        return (_bf16(x) if self.bf16_linear else x) @ m
+        return x @ m
 
     # ---------------------------------------------------------------- TimeMix
     def timemix_inputs(self, layer: int, x: torch.Tensor, previous: torch.Tensor):

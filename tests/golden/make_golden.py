@@ -18,10 +18,10 @@ What the vectors pin that no closed form does:
   from a carried state, with the final per-layer states;
 * ``model_tiny.npz`` -- C1's tiny model (weights regenerated from the seed by
   ``yufmusicgen_amd.synth``; a checksum guards the generator), prompt logits
-  and a 16-step greedy continuation.
+  and the 256-step greedy continuation of C1.
 
 Usage (from the repository root, never on the GPU box):
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [wkv rosa state_test tiny]   (default: all)
 """
 
 from __future__ import annotations
@@ -121,7 +121,7 @@ def model_tiny_golden() -> None:
         logits, state = model(prompt)
         last = logits[:, -1]
         greedy, greedy_logits = [], []
-        for _ in range(16):
+        for _ in range(256):
             token = torch.argmax(last, dim=-1)
             greedy.append(int(token))
             last, state = model.step(token, state)
@@ -133,9 +133,9 @@ def model_tiny_golden() -> None:
 
 if __name__ == "__main__":
     torch.manual_seed(0)
-    wkv_golden()
-    rosa_golden()
-    model_state_test_golden()
-    model_tiny_golden()
+    makers = {"wkv": wkv_golden, "rosa": rosa_golden, "state_test": model_state_test_golden,
+              "tiny": model_tiny_golden}
+    for name in sys.argv[1:] or list(makers):
+        makers[name]()
     for path in sorted(HERE.glob("*.np[zy]")) + sorted(HERE.glob("*.yuf")):
         print(f"{path.name}: {path.stat().st_size} bytes")

@@ -185,3 +185,28 @@ def test_v2_loader_rejects_malformed_files(bf16_yuf, tmp_path, case):
     assert err.value.status == -3, str(err.value)
     with pytest.raises((ValueError, KeyError)):
         read_yuf(bad)
+
+
+def test_header_json_exposes_midi_header_without_a_second_load(tiny_yuf):
+    """``yuf_ckpt_header_json``: the verbatim JSON the Rust loop reads as
+    ``checkpoint.header`` (midi_offset, midi_vocab_size, vocab, tokenizer_json;
+    vulkan/src/generation.rs:102-117), byte-identical to the file's header."""
+    path, cfg, _ = tiny_yuf
+    ck = Checkpoint.load(path)
+    raw = open(path, "rb").read()
+    (header_len,) = struct.unpack("<Q", raw[8:16])
+    assert ck.header_json.encode("utf-8") == raw[16:16 + header_len]
+    assert ck.version == 1
+    h = ck.header
+    assert h["midi"]["midi_offset"] == 260
+    assert h["midi"]["midi_vocab_size"] + 260 == cfg.vocab_size == h["model_config"]["vocab_size"]
+    assert len(h["midi"]["vocab"]) == h["midi"]["midi_vocab_size"]
+    assert "tokenizer_json" in h["midi"]
+
+
+def test_header_json_of_version_2_file(tmp_path):
+    cfg = PRESETS["state_test"]
+    path = tmp_path / "v2.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=4), linear_bf16=True)
+    ck = Checkpoint.load(path)
+    assert ck.version == 2 and ck.header["version"] == 2 and ck.header["payload_bytes"] > 0

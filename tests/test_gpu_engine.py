@@ -102,6 +102,34 @@ def test_state_save_load_reset_and_slots(state_test):
         eng.step([ck.config["vocab_size"]], slots=[0])
 
 
+def test_device_entry_points_report_bad_token_ids(state_test):
+    """An out-of-range id read by yuf_step_device / yuf_prefill_device is
+    reported by yuf_engine_take_error (once), never as a stale error of a later
+    host call; valid calls after it succeed."""
+    from yufmusicgen_amd._lib import YufError
+    ck, z = state_test
+    V = ck.config["vocab_size"]
+    eng = Engine(ck, max_streams=2, max_tokens=64)
+    logits = torch.empty(2, V, device="cuda")
+    slots = np.arange(2, dtype=np.int32)
+    bad = torch.tensor([3, V + 7], dtype=torch.int32, device="cuda")
+    eng.step_device(bad, logits, slots)
+    # The host path checks its own ids and does not report the device error.
+    eng.step(z["tokens"][:, 0])
+    with pytest.raises(YufError) as err:
+        eng.take_error()
+    assert err.value.status == -6
+    eng.take_error()  # cleared
+    good = torch.from_numpy(z["tokens"][:, :3].copy()).cuda()
+    eng.prefill_device(good, None, slots, logits="none")
+    eng.take_error()
+    neg = torch.tensor([[1, -1, 2], [4, 5, 6]], dtype=torch.int32, device="cuda")
+    eng.prefill_device(neg, None, slots, logits="none")
+    with pytest.raises(YufError):
+        eng.take_error()
+    eng.step(z["tokens"][:, 1])
+
+
 def test_chunked_prefill_equals_one_pass(state_test):
     """max_tokens smaller than n*T forces T-chunks that carry the state."""
     ck, z = state_test
@@ -196,12 +224,12 @@ def test_bf16_weights_engine_vs_bf16_oracle(tmp_path):
     to 2 layers (d = 1024, 16 x 64 heads, ROSA 256, V = 20480): 2 x 128 tokens
     of prefill (the bf16 large-tile kernel) and two decode steps (the bf16 decode
     kernel with LayerNorm prologues and the SiLU pair).  The oracle restates the
-    bf16 configuration (bf16 weights and projection inputs).  Two valid bf16
-    programs drift apart faster than fp32 ones (an activation near a bf16
-    rounding midpoint rounds either way, a 2^-8 step), so the bound is the
-    oracle's own float32 bf16 program's deviation from its float64 one (times
-    three, as for the fp32 wide model); and the engine must sit well inside the
-    distance between the bf16 and the fp32 configurations."""
+    bf16 configuration (the fp32 model on bf16-rounded weights).  The
+    activations enter the bf16 matrix cores as hi + lo parts (within 2^-16 of
+    their fp32 values), so the engine is held to the fp32 tolerances (logits
+    1e-3 absolute, states 1e-4 relative / 1e-4 absolute) and to 2 % of the
+    distance between the bf16-weight and the fp32-weight models, not to the
+    float32 program's own rounding."""
     import dataclasses
     cfg = dataclasses.replace(PRESETS["wide"], n_layers=2)
     weights = synth_weights(cfg, seed=8)
@@ -230,9 +258,15 @@ def test_bf16_weights_engine_vs_bf16_oracle(tmp_path):
         dev = float(np.abs(g - ref).max())
         prog = float(np.abs(ref32 - ref).max())
         effect = float(np.abs(fp - ref).max())
-        print(f"{name}: engine {dev:.3e}, float32 bf16 program {prog:.3e}, bf16 vs fp32 {effect:.3e}", flush=True)
-        assert dev <= 3.0 * prog + 1e-5, (name, dev, prog)
-        assert dev <= 0.5 * effect, (name, dev, effect)
+        print(f"{name}: engine {dev:.3e}, float32 program {prog:.3e}, bf16 vs fp32 weights {effect:.3e}", flush=True)
+        # The activations enter the bf16 matrix cores as hi + lo parts (within
+        # 2^-16 of fp32), so the engine sits above the float32 program's
+        # rounding but far inside the fp32 tolerances and the weight effect.
+        if name.startswith("logits"):
+            assert dev <= LOGIT_ATOL, (name, dev)
+        else:
+            np.testing.assert_allclose(g, ref, rtol=1e-4, atol=1e-4, err_msg=name)
+        assert dev <= 0.02 * effect, (name, dev, effect)
 
 
 def test_bf16_checkpoint_equals_rounded_f32_checkpoint(tmp_path):
@@ -303,6 +337,86 @@ def test_wide_decode_batch_vs_oracle(tmp_path):
         np.testing.assert_allclose(g, r.numpy(), rtol=0, atol=LOGIT_ATOL, err_msg=f"step {t}")
     blob = _states_from_blob(eng, [0, 17, 39])
     np.testing.assert_allclose(blob, state_to_blob(state)[[0, 17, 39]], rtol=1e-4, atol=1e-4)
+
+
+def test_c4_shape_64_streams_32_steps_vs_oracle(tmp_path):
+    """The production decode shape of C4: 64 streams of the 0.1B model (four
+    full 16-row tiles of every decode product, the M = 64 wide LM head, the
+    K-split FFN output and the fused ROSA-out), a short prompt, then 32
+    teacher-forced decode steps replayed from the step graph, against the
+    float64 oracle: logits within 1e-3 at every step, identical greedy ids
+    wherever the top-2 gap exceeds 1e-3, carried states within 1e-4."""
+    cfg = PRESETS["0.1b"]
+    weights = synth_weights(cfg, seed=21)
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, weights)
+    n, prompt_len, steps = 64, 8, 32
+    tokens = uniform_tokens(22, n, prompt_len, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=n, max_tokens=n * prompt_len)
+    got = eng.prefill(tokens, logits="last")
+    oracle = OracleModel(cfg.to_dict(), weights)
+    ref, state = oracle.forward(tokens)
+    np.testing.assert_allclose(got, ref.numpy()[:, -1], rtol=0, atol=LOGIT_ATOL)
+    nxt = uniform_tokens(23, n, steps, cfg.vocab_size)
+    worst = 0.0
+    for t in range(steps):
+        g = eng.step(nxt[:, t])
+        r, state = oracle.step(nxt[:, t], state)
+        r = r.numpy()
+        worst = max(worst, float(np.abs(g - r).max()))
+        np.testing.assert_allclose(g, r, rtol=0, atol=LOGIT_ATOL, err_msg=f"step {t}")
+        top2 = np.sort(r, axis=1)[:, -2:]
+        sure = top2[:, 1] - top2[:, 0] > LOGIT_ATOL
+        assert np.array_equal(np.argmax(g, 1)[sure], np.argmax(r, 1)[sure]), f"step {t}"
+    print(f"64 streams x {steps} steps: worst logit deviation {worst:.2e}", flush=True)
+    blob = _states_from_blob(eng, range(n))
+    np.testing.assert_allclose(blob, state_to_blob(state), rtol=1e-4, atol=1e-4)
+
+
+def test_c5_bf16_24_layers_vs_fp32_oracle(tmp_path):
+    """C5 as configured: 24 layers, d = 1024, 16 x 64
+    heads, ROSA 256, V = 20480, bf16 projection weights (a version-2 .yuf) with
+    fp32 WKV / ROSA state, against the reference's fp32 program on the same
+    bf16-valued weights -- every nn.Linear weight and the tied LM head, the
+    embedding gather in f32 (model.py:406-431, evaluated in float64 by the oracle):
+    logits within the configuration's 2e-2 at every position and step, and
+    identical greedy ids wherever the reference's top-2 gap exceeds 2e-2.
+    Beside it the fp32 configurations' logit tolerance: the activations keep
+    fp32 precision up to the 2^-16 of their bf16 hi + lo split, so the engine
+    stays within 1e-3 of the reference."""
+    cfg = PRESETS["wide"]
+    weights = synth_weights(cfg, seed=31)
+    path = tmp_path / "c5.yuf"
+    write_yuf(path, cfg, weights, linear_bf16=True)
+    tokens = prompt_tokens(32, 2, 64, cfg.vocab_size)
+    nxt = uniform_tokens(33, 2, 2, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=2, max_tokens=128, weight_dtype="bf16")
+    got = [eng.prefill(tokens, logits="all")] + [eng.step(nxt[:, t]) for t in range(2)]
+
+    from yufmusicgen_amd.checkpoint import read_yuf
+    _, stored = read_yuf(path)  # the bf16 weights of the file, widened to f32
+
+    def run(model):
+        out, st = model.forward(tokens)
+        outs = [out.numpy().astype(np.float64)]
+        for t in range(2):
+            out, st = model.step(nxt[:, t], st)
+            outs.append(out.numpy().astype(np.float64))
+        return outs
+
+    # bf16_linear also rounds the tied LM head (the file keeps the embedding in
+    # f32; the engine's bf16 mode runs the head from a bf16 copy).
+    ref = run(OracleModel(cfg.to_dict(), stored, bf16_linear=True))
+    ref32 = run(OracleModel(cfg.to_dict(), stored, dtype=torch.float32, bf16_linear=True))
+    tol = 2e-2
+    for i, (g, r, r32) in enumerate(zip(got, ref, ref32)):
+        dev, prog = float(np.abs(g - r).max()), float(np.abs(r32 - r).max())
+        print(f"C5 bf16 output {i}: engine vs fp32 reference {dev:.3e}, float32 program {prog:.3e}", flush=True)
+        np.testing.assert_allclose(g, r, rtol=0, atol=tol, err_msg=f"output {i}")
+        top2 = np.sort(r, axis=-1)[..., -2:]
+        sure = top2[..., 1] - top2[..., 0] > tol
+        assert np.array_equal(np.argmax(g, -1)[sure], np.argmax(r, -1)[sure]), f"output {i}"
+        assert dev <= LOGIT_ATOL, (i, dev, prog)
 
 
 def test_device_sampling():
@@ -393,7 +507,7 @@ def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, pre
         np.testing.assert_array_equal(graph_eng.step(ids), eager_eng.step(ids))
 
 
-@pytest.mark.parametrize("preset,n", [("0.1b", 40), ("d256_rosa256", 5)])
+@pytest.mark.parametrize("preset,n", [("0.1b", 40), ("0.1b", 64), ("d256_rosa256", 5)])
 def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n):
     """The folded decode kernels (second low-rank stage inside the WKV step,
     ROSA step as the ROSA-out prologue with the tile's last workgroup writing

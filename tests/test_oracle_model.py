@@ -105,9 +105,8 @@ def test_bf16_rounding_of_the_bf16_oracle():
 
 def test_bf16_oracle_rounds_projection_operands_only():
     """bf16_linear rounds the nn.Linear weights and the LM head, never the
-    embedding gather, the norms, the recurrence parameters or the biases; with
-    weights and a batch made of bf16 values the first projection's inputs
-    change only through the rounding of activations."""
+    embedding gather, the norms, the recurrence parameters or the biases, and
+    then computes exactly as the fp32 model does on those weights."""
     cfg = PRESETS["tiny"]
     weights = synth_weights(cfg, seed=3)
     model = OracleModel(cfg.to_dict(), weights, bf16_linear=True)
@@ -130,3 +129,8 @@ def test_bf16_oracle_rounds_projection_operands_only():
     b, _ = plain.forward(ids)
     rel = float((a - b).abs().max() / b.abs().max())
     assert 1e-4 < rel < 5e-2, rel
+    # Activations are not rounded: the plain model run on the rounded weights
+    # is the same program.
+    rounded = OracleModel(cfg.to_dict(), {n: v.numpy() for n, v in model.w.items()})  # incl. the rounded head
+    c, _ = rounded.forward(ids)
+    assert torch.equal(a, c)

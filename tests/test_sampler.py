@@ -66,6 +66,35 @@ def test_generation_mask_then_sample():
     assert got == expect and got >= 260
 
 
+def test_generation_mask_hand_derived_vectors():
+    """Expected vectors written out by hand from cli/generate.py:139-148 (and
+    generation.rs:195-203), not from any restatement: with V = 270, ids 0..259
+    are -inf, ids 260..269 keep their logit; EOS (id 2) is -inf at index 15 and
+    keeps its logit from index 16 on; blocked raw id 5 means token 265."""
+    from yufmusicgen_amd.engine import generation_mask as native_mask
+
+    V = 270
+    x = np.arange(V, dtype=np.float32) * 0.5 - 7.0  # distinct finite logits
+    ninf = -np.inf
+    for index, eos_kept in ((0, False), (15, False), (16, True), (17, True)):
+        expect = np.full(V, ninf, np.float32)
+        expect[260:] = x[260:]
+        if eos_kept:
+            expect[2] = x[2]  # -6.0
+        expect_blocked = expect.copy()
+        expect_blocked[265] = ninf
+        for got in (generation_mask(torch.from_numpy(x), index=index).numpy(), native_mask(x, index)):
+            np.testing.assert_array_equal(got, expect)
+        for got in (generation_mask(torch.from_numpy(x), index=index, blocked_raw_ids=(5,)).numpy(),
+                    native_mask(x, index, (5,))):
+            np.testing.assert_array_equal(got, expect_blocked)
+    # Spot values, independent of the loop above.
+    m15, m16 = native_mask(x, 15), native_mask(x, 16)
+    assert m15[259] == ninf and m15[260] == x[260] == 123.0 and m15[2] == ninf
+    assert m16[2] == -6.0 and m16[3] == ninf and m16[1] == ninf
+    assert native_mask(x, 40, (5,))[265] == ninf and native_mask(x, 40, (5,))[264] == x[264]
+
+
 @pytest.mark.parametrize("index", [0, 15, 16, 40])
 @pytest.mark.parametrize("blocked", [(), (0, 5, 127)])
 def test_native_generation_mask_matches_oracle(index, blocked):

@@ -55,6 +55,9 @@ SIGNATURES = {
     "yuf_ckpt_tensor": (ctypes.c_int, [c_void_p, ctypes.c_char_p, ctypes.POINTER(c_float_p),
                                        ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int32),
                                        ctypes.POINTER(ctypes.c_int64)]),
+    "yuf_ckpt_header_json": (ctypes.c_int, [c_void_p, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_size_t),
+                                            ctypes.POINTER(ctypes.c_uint32)]),
+    "yuf_engine_take_error": (ctypes.c_int, [c_void_p]),
     "yuf_engine_create": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.POINTER(c_void_p)]),
     "yuf_engine_create_ex": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(c_void_p)]),
     "yuf_engine_destroy": (None, [c_void_p]),

@@ -2,8 +2,8 @@
 //
 // Container (vulkan/scripts/export_checkpoint.py:32-146; checks of
 // vulkan/src/checkpoint.rs:90-149):
-//   b"YUFM" | u32 LE version = 1 | u64 LE header_len | UTF-8 JSON | f32 LE payload
-// The payload size must equal 4 * sum(tensors[].count) exactly.
+//   b"YUFM" | u32 LE version (1 or 2) | u64 LE header_len | UTF-8 JSON | payload
+// Version 1: an f32 LE payload whose size must equal 4 * sum(tensors[].count).
 // Version 2 (this build's extension for bf16 weights): tensor entries carry a
 // "dtype" ("f32" | "bf16") and a byte "offset" into the payload (a multiple of
 // the element size), the header a "payload_bytes" that the file size must
@@ -231,6 +231,7 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
     std::string err;
     json::Parser parser(header.data(), header.data() + header.size());
     if (!parser.parse(root, err)) return fail(YUF_ERR_FORMAT, "invalid .yuf header JSON: " + err);
+    ck.version = version;
     const json::Value *fmt = root.get("format");
     if (!fmt || fmt->kind != json::Value::String || fmt->str != "yufmusicgen-checkpoint")
         return fail(YUF_ERR_FORMAT, "unexpected .yuf payload format");
@@ -341,6 +342,7 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
     if (it == ck.tensors.end() || it->second.dims.size() != 2 || it->second.dims[0] != s.d)
         return fail(YUF_ERR_FORMAT, "checkpoint has no usable blocks.0.time_mix.w1");
     s.low_rank = (int)it->second.dims[1];
+    ck.header_json = std::move(header);
     return YUF_OK;
 }
 
@@ -402,6 +404,14 @@ extern "C" int yuf_ckpt_tensor(const yuf_ckpt *ckpt, const char *name, const flo
     if (ndim) *ndim = (int32_t)it->second.dims.size();
     if (dims)
         for (size_t i = 0; i < it->second.dims.size() && i < 8; ++i) dims[i] = it->second.dims[i];
+    return YUF_OK;
+}
+
+extern "C" int yuf_ckpt_header_json(const yuf_ckpt *ckpt, const char **json, size_t *len, uint32_t *version) {
+    if (!ckpt || !json) return yuf::fail(YUF_ERR_INVALID, "yuf_ckpt_header_json: null argument");
+    *json = ckpt->ck.header_json.c_str();
+    if (len) *len = ckpt->ck.header_json.size();
+    if (version) *version = ckpt->ck.version;
     return YUF_OK;
 }
 

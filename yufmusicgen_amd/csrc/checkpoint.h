@@ -1,6 +1,7 @@
 // Host-side checkpoint representation shared by the loader and the engine.
 #pragma once
 
+#include <cstdint>
 #include <map>
 #include <string>
 #include <vector>
@@ -27,6 +28,8 @@ struct Checkpoint {
     ModelShape shape;
     std::map<std::string, TensorInfo> tensors;
     std::vector<float> data;
+    std::string header_json;  // the file's UTF-8 JSON header, verbatim
+    uint32_t version = 0;
     // Host pointer to a tensor, checking its shape when `dims` is non-empty.
     const float *tensor(const std::string &name, const std::vector<long long> &dims, std::string &err) const;
 };

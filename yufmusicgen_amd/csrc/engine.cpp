@@ -83,7 +83,10 @@ struct Engine {
     bool decode_fusion = true;                                 // YUF_DECODE_FUSION=0: separate low-rank GEMM and ROSA step
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
     size_t gemm_ws_floats = 0;
-    int *slots_dev = nullptr, *tokens_dev = nullptr, *bad_dev = nullptr;
+    // Out-of-range token flags set by the embedding kernel: bad_host for the
+    // host-buffer entry points (ids already validated on the host), bad_dev
+    // for the device entry points (read by yuf_engine_take_error).
+    int *slots_dev = nullptr, *tokens_dev = nullptr, *bad_dev = nullptr, *bad_host = nullptr;
     int *rosa_count = nullptr;  // [max_streams]: 16-row tile counters of the fused ROSA-out kernel, by first stream
     int *slots_host = nullptr;  // pinned
     std::vector<int> last_slots;
@@ -348,6 +351,7 @@ struct Act {
     float *h, *xn, *mix, *r, *k, *v, *wr, *al, *g, *lr, *y, *z, *rosa3, *rread, *ffn, *hl;
     float *rz, *rcarry, *rends;  // segmented ROSA scratch (segment rows of kRosaSeg tokens)
     const int *tokens, *slots;
+    int *bad;     // out-of-range token flag the embedding sets
     int *rcount;  // fused ROSA-out tile counters of this group of streams
     float *kpart;  // FFN-out K-split partials of these streams, planes kplane floats apart
     size_t kplane;
@@ -369,6 +373,7 @@ Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
     a.rz = e.rz + seg0; a.rcarry = e.rcarry + seg0; a.rends = e.rends + seg0;
     a.tokens = e.tokens_dev + m0;
     a.slots = e.slots_dev + s0;
+    a.bad = e.bad_dev;
     a.rcount = e.rosa_count + s0;
     a.kpart = e.kpart + (size_t)s0 * d;
     a.kplane = (size_t)e.max_streams * d;
@@ -394,7 +399,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     const int M = n * Tc, d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4 * s.d;
     const size_t plane = (size_t)e.max_tokens * d, lplane = (size_t)e.max_tokens * L;
     hipStream_t st = a.st;
-    ENG_TRY(launch_embed(a.tokens, M, e.emb, d, V, a.h, e.bad_dev, st), "embed");
+    ENG_TRY(launch_embed(a.tokens, M, e.emb, d, V, a.h, a.bad, st), "embed");
     // Decode: the FFN output product is split over K into kFfnParts products
     // (four times the workgroups); the partial sums stay in a.kpart until the
     // next layer's ln_shift (or, after the last layer, add_parts) adds them to h.
@@ -552,6 +557,12 @@ int upload_slots(Engine &e, int n, const int32_t *slots) {
     return YUF_OK;
 }
 
+// The embedding's error flag for a call whose ids are at `tokens`: the host
+// entry points stage their (validated) ids in host_tokens.
+int *flag_for(Engine &e, const int32_t *tokens) {
+    return tokens == static_cast<const int32_t *>(e.host_tokens.p) ? e.bad_host : e.bad_dev;
+}
+
 // Prefill n x T tokens (device pointer), splitting T into chunks of at most max_tokens / n.
 int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logits_dev, int mode) {
     const int tc_max = std::max(1, e.max_tokens / n);
@@ -569,7 +580,9 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         }
         const bool last_chunk = t0 + tc >= T;
         const int chunk_mode = mode == YUF_LOGITS_ALL ? YUF_LOGITS_ALL : (last_chunk ? mode : YUF_LOGITS_NONE);
-        int rc = forward_pass(e, act_at(e, e.stream, 0, tc), n, tc, logits_dev, chunk_mode, T, t0);
+        Act a = act_at(e, e.stream, 0, tc);
+        a.bad = flag_for(e, tokens_dev);
+        int rc = forward_pass(e, a, n, tc, logits_dev, chunk_mode, T, t0);
         if (rc != YUF_OK) return rc;
     }
     return YUF_OK;
@@ -605,8 +618,10 @@ int drop_step_graphs(Engine &e) {
 }
 
 // One decode step (T = 1, last-position logits) of n streams whose slots are
-// already on the device, replayed from captured graphs (kernels and one
-// device-to-device copy only: no memset nodes, no host synchronisation).
+// already on the device, replayed from captured graphs (kernel nodes only: no
+// memset or copy nodes, no host synchronisation; the graphs read the caller's
+// token ids in place and are captured again when n, the token pointer or the
+// logits pointer changes).
 // With one branch the whole step is one graph.  With G > 1 the streams are
 // split into G groups whose layers are G graphs launched on G HIP streams
 // (forked from and joined back into the engine stream with events, so the
@@ -626,6 +641,7 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
             rc = capture(e.stream, [&]() {
                 Act a = act_at(e, e.stream, 0, 1);
                 a.tokens = tokens_dev;
+                a.bad = flag_for(e, tokens_dev);
                 return forward_pass(e, a, n, 1, logits_dev, YUF_LOGITS_LAST, 1, 0);
             }, &e.step_exec[0]);
         } else {
@@ -635,6 +651,7 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
                 rc = capture(st, [&]() {
                     Act a = act_at(e, st, s0, 1);
                     a.tokens = tokens_dev + s0;
+                    a.bad = flag_for(e, tokens_dev);
                     return forward_pass(e, a, s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
                 }, &e.step_exec[g]);
             }
@@ -817,17 +834,19 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
                          &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.rends, &e.kpart};
         for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
     }
-    const size_t io_bytes = 256 * 4 + (size_t)(2 * max_streams + max_tokens + 1) * sizeof(int);
+    const size_t io_bytes = 256 * 5 + (size_t)(2 * max_streams + max_tokens + 2) * sizeof(int);
     ENG_TRY(hipMalloc(&e.io.p, io_bytes), "io alloc");
     {
         char *cur = static_cast<char *>(e.io.p);
         e.slots_dev = carve<int>(cur, max_streams);
         e.tokens_dev = carve<int>(cur, max_tokens);
         e.bad_dev = carve<int>(cur, 1);
+        e.bad_host = carve<int>(cur, 1);
         e.rosa_count = carve<int>(cur, max_streams);
     }
     ENG_TRY(hipHostMalloc(reinterpret_cast<void **>(&e.slots_host), max_streams * sizeof(int)), "pinned alloc");
     ENG_TRY(hipMemsetAsync(e.bad_dev, 0, sizeof(int), e.stream), "flag clear");
+    ENG_TRY(hipMemsetAsync(e.bad_host, 0, sizeof(int), e.stream), "flag clear");
     // Tile counters of the fused ROSA-out decode kernel: zero here, and every
     // launch leaves them at zero (outside any captured graph).
     ENG_TRY(hipMemsetAsync(e.rosa_count, 0, (size_t)max_streams * sizeof(int), e.stream), "counter clear");
@@ -916,13 +935,28 @@ extern "C" int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T, 
         ENG_TRY(hipMemcpyAsync(logits, e.host_logits.p, n_logits * sizeof(float), hipMemcpyDeviceToHost, e.stream),
                 "logits download");
     int bad = 0;
-    ENG_TRY(hipMemcpyAsync(&bad, e.bad_dev, sizeof(int), hipMemcpyDeviceToHost, e.stream), "flag read");
+    ENG_TRY(hipMemcpyAsync(&bad, e.bad_host, sizeof(int), hipMemcpyDeviceToHost, e.stream), "flag read");
     ENG_TRY(hipStreamSynchronize(e.stream), "prefill sync");
     if (bad) {
-        ENG_TRY(hipMemsetAsync(e.bad_dev, 0, sizeof(int), e.stream), "flag clear");
-        return fail(YUF_ERR_RANGE, "a device-side token id was out of range (its embedding was zeroed)");
+        ENG_TRY(hipMemsetAsync(e.bad_host, 0, sizeof(int), e.stream), "flag clear");
+        ENG_TRY(hipStreamSynchronize(e.stream), "flag clear sync");
+        return fail(YUF_ERR_RANGE, "a token id was out of range on the device (its embedding was zeroed)");
     }
     return YUF_OK;
+}
+
+extern "C" int yuf_engine_take_error(yuf_engine *eng) {
+    using namespace yuf;
+    if (!eng) return fail(YUF_ERR_INVALID, "null engine");
+    Engine &e = eng->e;
+    int bad = 0;
+    ENG_TRY(hipMemcpyAsync(&bad, e.bad_dev, sizeof(int), hipMemcpyDeviceToHost, e.stream), "flag read");
+    ENG_TRY(hipStreamSynchronize(e.stream), "flag read sync");
+    if (!bad) return YUF_OK;
+    ENG_TRY(hipMemsetAsync(e.bad_dev, 0, sizeof(int), e.stream), "flag clear");
+    ENG_TRY(hipStreamSynchronize(e.stream), "flag clear sync");
+    return fail(YUF_ERR_RANGE, "a device-side token id was out of range in a yuf_prefill_device / yuf_step_device call "
+                               "(its embedding was zeroed)");
 }
 
 extern "C" int yuf_step_device(yuf_engine *eng, int n, const int32_t *slots, const int32_t *tokens_dev,

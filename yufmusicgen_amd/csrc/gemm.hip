@@ -21,12 +21,17 @@
 // then 32 "gate" rows; output silu(in) * gate).
 //
 // bf16 weights (GemmParams::Wh, the C5 configuration's weight type): the
-// large-tile and decode kernels take a WB flag.  W streams as bf16, A stays
-// fp32 in memory and is rounded to bf16 (round to nearest even, the gfx950
-// v_cvt_pk_bf16_f32) as it enters the matrix core; products accumulate in fp32
-// with v_mfma_f32_16x16x32_bf16 (lane l: A[m = l % 16][k = 8 (l / 16) + j],
+// large-tile and decode kernels take a WB flag.  W streams as bf16 and A stays
+// fp32 in memory.  As A enters the matrix core it is split into two bf16
+// parts, hi = bf16(a) and lo = bf16(a - hi) (round to nearest even, the gfx950
+// v_cvt_pk_bf16_f32), and each k-step runs two v_mfma_f32_16x16x32_bf16,
+// hi x W then lo x W (lane l: A[m = l % 16][k = 8 (l / 16) + j],
 // B[k = 8 (l / 16) + j][n = l % 16], j < 8; accumulator layout as for
-// v_mfma_f32_16x16x4f32), so the epilogues are shared.  Needs K % 8 == 0.
+// v_mfma_f32_16x16x4f32), so the epilogues are shared.  A product of two bf16
+// values is exact in fp32 and |a - hi - lo| <= 2^-16 |a|, so the result is the
+// fp32 product A x bf16(W) up to fp32 accumulation order: the activations keep
+// fp32 precision (a single bf16 rounding of A moves C5 logits by up to ~0.2
+// over 24 layers, against the configuration's 2e-2).  Needs K % 8 == 0.
 #include <algorithm>
 #include <type_traits>
 
@@ -226,6 +231,18 @@ __device__ __forceinline__ bf16x8 to_bf16x8(floatx4 lo, floatx4 hi) {
     }
     return r;
 }
+
+// The two bf16 parts of eight fp32 values: hi = bf16(x), lo = bf16(x - hi).
+__device__ __forceinline__ void split_bf16x8(floatx4 x0, floatx4 x1, bf16x8 &hi, bf16x8 &lo) {
+    hi = to_bf16x8(x0, x1);
+    floatx4 r0, r1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        r0[q] = x0[q] - (float)hi[q];
+        r1[q] = x1[q] - (float)hi[4 + q];
+    }
+    lo = to_bf16x8(r0, r1);
+}
 constexpr int kBigBM = 256, kBigThreads = 512;
 // K tile: 32 where the accumulators leave room for the larger load set, else 16.
 template <int BN> constexpr int big_bk() { return BN >= 256 ? 16 : 32; }
@@ -293,16 +310,22 @@ __device__ __forceinline__ void big_store_h(const BigLoadH<ROWS> &t, __bf16 *lds
     }
 }
 
-// fp32 A tile (32 k) rounded to bf16 on its way into LDS.
+// fp32 A tile (32 k) split into its bf16 parts on the way into LDS: hi into
+// `hi`, lo = bf16(a - hi) into `lo` (same layout).
 template <int ROWS>
-__device__ __forceinline__ void big_store_a_h(const BigLoad<ROWS, 32> &t, __bf16 *lds, int tid) {
+__device__ __forceinline__ void big_store_a_h(const BigLoad<ROWS, 32> &t, __bf16 *hi, __bf16 *lo, int tid) {
     typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int i = 0; i < BigLoad<ROWS, 32>::kPer; ++i) {
         const int q = tid + i * kBigThreads;
         if (q < BigLoad<ROWS, 32>::kF4) {
-            const bf16x4 h = {(__bf16)t.v[i].x, (__bf16)t.v[i].y, (__bf16)t.v[i].z, (__bf16)t.v[i].w};
-            *reinterpret_cast<bf16x4 *>(lds + (q / 8) * kLdh + (q % 8) * 4) = h;
+            const float4 x = t.v[i];
+            const bf16x4 h = {(__bf16)x.x, (__bf16)x.y, (__bf16)x.z, (__bf16)x.w};
+            const bf16x4 l = {(__bf16)(x.x - (float)h[0]), (__bf16)(x.y - (float)h[1]), (__bf16)(x.z - (float)h[2]),
+                              (__bf16)(x.w - (float)h[3])};
+            const int o = (q / 8) * kLdh + (q % 8) * 4;
+            *reinterpret_cast<bf16x4 *>(hi + o) = h;
+            *reinterpret_cast<bf16x4 *>(lo + o) = l;
         }
     }
 }
@@ -320,13 +343,14 @@ template <int BN, bool STAGED, bool WB>
 __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int per_xcd) {
     constexpr int WN = BN / 2, NT = WN / 16;
     constexpr int kBigBK = WB ? 32 : big_bk<BN>(), kBigLd = kBigBK + 4;
-    constexpr int kLdsFloats = WB ? (2 * (kBigBM + BN) * kLdh) / 2 : 2 * (kBigBM + BN) * kBigLd;
+    constexpr int kLdsFloats = WB ? (2 * (2 * kBigBM + BN) * kLdh) / 2 : 2 * (kBigBM + BN) * kBigLd;
     static_assert(kLdsFloats >= kBigThreads / 64 * 16 * (WN + 4), "LDS too small for the staged epilogue");
     __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
     float(*As)[kBigBM * kBigLd] = reinterpret_cast<float(*)[kBigBM * kBigLd]>(lds);
     float(*Bs)[BN * kBigLd] = reinterpret_cast<float(*)[BN * kBigLd]>(lds + 2 * kBigBM * kBigLd);
-    __bf16 *Ah = reinterpret_cast<__bf16 *>(lds);  // WB: [2][kBigBM * kLdh], then [2][BN * kLdh]
-    __bf16 *Bh = Ah + 2 * kBigBM * kLdh;
+    __bf16 *Ah = reinterpret_cast<__bf16 *>(lds);  // WB: A hi [2][kBigBM * kLdh], A lo [2][kBigBM * kLdh],
+    __bf16 *Al = Ah + 2 * kBigBM * kLdh;            // then W [2][BN * kLdh]
+    __bf16 *Bh = Al + 2 * kBigBM * kLdh;
 
     const GemmParams &p = g.p[blockIdx.y];
     const int tiles_n = g.tiles_n[blockIdx.y];
@@ -358,7 +382,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
     };
     auto store_tiles = [&](int buf) {
         if constexpr (WB) {
-            big_store_a_h(ta, Ah + buf * kBigBM * kLdh, tid);
+            big_store_a_h(ta, Ah + buf * kBigBM * kLdh, Al + buf * kBigBM * kLdh, tid);
             big_store_h(tb, Bh + buf * BN * kLdh, tid);
         } else {
             big_store(ta, As[buf], tid);
@@ -378,18 +402,23 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
             load_w((kt + 1) * kBigBK);
         }
         if constexpr (WB) {
-            // One 32-k step: a lane's 8 k of a row are one ds_read_b128.
-            const __bf16 *Ac = Ah + cur * kBigBM * kLdh, *Bc = Bh + cur * BN * kLdh;
-            bf16x8 af[4], bf[NT];
+            // One 32-k step: a lane's 8 k of a row are one ds_read_b128 per part.
+            const __bf16 *Ac = Ah + cur * kBigBM * kLdh, *Alc = Al + cur * kBigBM * kLdh, *Bc = Bh + cur * BN * kLdh;
+            bf16x8 af[4], al[4], bf[NT];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const bf16x8 *>(Ac + (wm * 64 + i * 16 + li) * kLdh + 8 * g4);
+            for (int i = 0; i < 4; ++i) {
+                af[i] = *reinterpret_cast<const bf16x8 *>(Ac + (wm * 64 + i * 16 + li) * kLdh + 8 * g4);
+                al[i] = *reinterpret_cast<const bf16x8 *>(Alc + (wm * 64 + i * 16 + li) * kLdh + 8 * g4);
+            }
 #pragma unroll
             for (int j = 0; j < NT; ++j) bf[j] = *reinterpret_cast<const bf16x8 *>(Bc + (wn * WN + j * 16 + li) * kLdh + 8 * g4);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < NT; ++j)
+                for (int j = 0; j < NT; ++j) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bf[j], acc[i][j], 0, 0, 0);
+                }
         }
 #pragma unroll
         for (int h = 0; h < (WB ? 0 : kBigBK / 16); ++h) {  // 16 k per half: one ds_read_b128 per operand fragment
@@ -796,10 +825,13 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
             if constexpr (WB) {
 #pragma unroll
                 for (int i = 0; i < MI; ++i) {
-                    const bf16x8 ah = to_bf16x8(a[s][i][0], a[s][i][AH - 1]);
+                    bf16x8 ah, al;
+                    split_bf16x8(a[s][i][0], a[s][i][AH - 1], ah, al);
 #pragma unroll
-                    for (int t = 0; t < NT; ++t)
+                    for (int t = 0; t < NT; ++t) {
                         acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, __builtin_bit_cast(bf16x8, b[s][t]), acc[t][i], 0, 0, 0);
+                        acc[t][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, __builtin_bit_cast(bf16x8, b[s][t]), acc[t][i], 0, 0, 0);
+                    }
                 }
             } else {
 #pragma unroll

@@ -44,6 +44,28 @@ class Checkpoint:
         check(lib().yuf_ckpt_config(self._h, ctypes.byref(c)))
         return _config_dict(c)
 
+    @property
+    def header_json(self) -> str:
+        """The file's JSON header verbatim (``checkpoint.header``, checkpoint.rs:60-81)."""
+        text = ctypes.c_char_p()
+        size = ctypes.c_size_t()
+        version = ctypes.c_uint32()
+        check(lib().yuf_ckpt_header_json(self._h, ctypes.byref(text), ctypes.byref(size), ctypes.byref(version)))
+        return ctypes.string_at(text, size.value).decode("utf-8")
+
+    @property
+    def header(self) -> dict:
+        import json
+
+        return json.loads(self.header_json)
+
+    @property
+    def version(self) -> int:
+        text = ctypes.c_char_p()
+        version = ctypes.c_uint32()
+        check(lib().yuf_ckpt_header_json(self._h, ctypes.byref(text), None, ctypes.byref(version)))
+        return int(version.value)
+
     def tensor(self, name: str) -> np.ndarray:
         """``Checkpoint::tensor`` + ``tensor_dims`` (checkpoint.rs:151-168); a copy."""
         data = c_float_p()
@@ -157,6 +179,11 @@ class Engine:
         n = tokens_dev.shape[0]
         check(lib().yuf_step_device(self._h, n, self._slots(n, slots).ctypes.data, tokens_dev.data_ptr(),
                                     logits_dev.data_ptr()))
+
+    def take_error(self) -> None:
+        """Raise if a device entry point read an out-of-range token id since the
+        last check (``yuf_engine_take_error``; synchronises the engine stream)."""
+        check(lib().yuf_engine_take_error(self._h))
 
     def close(self) -> None:
         if self._h:
