@@ -284,12 +284,17 @@ uint32_t yuf_rng_next_u32(yuf_rng *rng);
 /* 53-bit uniform in [0,1) from two words (hi << 32 | lo). */
 double yuf_rng_next_uniform(yuf_rng *rng);
 
-/* Host sampling over V logits, token-for-token what torch's CPU
- * `sample_token` draws under the same seed: temperature <= 0 -> argmax
- * (first maximum); otherwise scale, optional top_k (> 0: keep the k largest),
- * sort descending, softmax, drop where cumulative - p > top_p, renormalise,
- * and torch.multinomial's single-sample path argmax(p / q), q ~ Exp(1).
- * Returns the token id, or a negative yuf_status. */
+/* Host sampling over V logits following torch's CPU `sample_token` under the
+ * same seed: temperature <= 0 -> argmax (first maximum); otherwise scale,
+ * optional top_k (> 0: keep the k largest), sort descending, softmax, drop
+ * where cumulative - p > top_p, renormalise, and torch.multinomial's
+ * single-sample path argmax(p / q), q ~ Exp(1) -- V draws from the generator
+ * per call, as torch consumes them.  The draws are bit-identical to torch's;
+ * the softmax uses correctly rounded float exps and sums in the 16-lane order
+ * of torch's AVX-512 kernel (the reference's Rust sampler assumes 8 lanes,
+ * sampler.rs:145-170), so on hosts where torch dispatches another vector
+ * width a token can differ from torch's only where two candidates tie to the
+ * last bit.  Returns the token id, or a negative yuf_status. */
 int32_t yuf_sample(const float *logits, int V, float temperature, float top_p, int top_k,
                    yuf_rng *rng);
 /* First index of the maximum (torch.argmax semantics). */
@@ -305,12 +310,47 @@ int yuf_generation_mask(const float *logits, int V, int index, int midi_offset, 
                         float *allowed_out);
 
 /* Device sampling for n streams at once (no logits copy to the host):
- * temperature <= 0 -> argmax; otherwise top_k in [1, 64] largest scaled
- * logits, softmax over them and a Gumbel-max draw from a counter-based
- * generator keyed by (seed, counter, stream index).  Not bit-compatible with
- * torch (use yuf_sample for that).  logits_dev [n, V]; tokens_dev [n] int32. */
+ * temperature <= 0 -> argmax; otherwise the top_k in [1, 64] largest scaled
+ * logits, softmax over them and a draw argmax p / q with q = -log u, u from a
+ * counter-based generator keyed by (seed, counter, stream, token id) -- the
+ * distribution of torch.multinomial, not its stream.  logits_dev [n, V];
+ * tokens_dev [n] int32.  yuf_sample_device_masked(..., midi_offset = -1,
+ * top_p = 1, exp_draws_dev = NULL, ...) with the same arguments. */
 int yuf_sample_device(int n, int V, const float *logits_dev, float temperature, int top_k,
                       uint64_t seed, uint64_t counter, int32_t *tokens_dev, void *stream);
+
+/* The generation loop's mask and sampler on the device, for n streams at once
+ * (vulkan/src/generation.rs:195-203 then sampler.rs:131-256; Python
+ * cli/generate.py:139-154): no logits copy, no host sort.
+ *   mask: midi_offset >= 0 applies yuf_generation_mask's rule per stream --
+ *     ids below midi_offset and midi_offset + blocked_raw_ids[j] are -inf, the
+ *     EOS id keeps its logit once the stream's index >= min_before_eos; the
+ *     index is index_dev[s] (device [n] int32) or, if index_dev is NULL, the
+ *     host `index` for every stream.  blocked_raw_ids: host array, at most 256
+ *     raw ids, each below 32768 and midi_offset + id < V.  midi_offset < 0: no
+ *     mask.
+ *   draw: temperature <= 0 -> the first maximum of the masked logits;
+ *     otherwise top_k in [1, 64] (the k largest masked logits / temperature),
+ *     then top_p and the draw exactly as yuf_sample computes them.
+ *     exp_draws_dev (device [n, top_k] float) and first_zero_dev (device [n]
+ *     int32), filled from each stream's generator by yuf_rng_exp_draws, make
+ *     the token equal yuf_sample(masked logits, temperature, top_p, top_k,
+ *     rng) for the same generator state; with exp_draws_dev NULL the
+ *     counter-based draws of yuf_sample_device are used (first_zero_dev
+ *     ignored).
+ * Asynchronous on `stream`; tokens_dev [n] int32. */
+int yuf_sample_device_masked(int n, int V, const float *logits_dev, float temperature, float top_p,
+                             int top_k, int midi_offset, int eos_id, int min_before_eos, int index,
+                             const int32_t *index_dev, const int32_t *blocked_raw_ids, int n_blocked,
+                             const float *exp_draws_dev, const int32_t *first_zero_dev, uint64_t seed,
+                             uint64_t counter, int32_t *tokens_dev, void *stream);
+
+/* The generator draws one host sample consumes, for the device's exact mode:
+ * takes V uniforms from `rng` (exactly what yuf_sample takes for V logits),
+ * writes q_out[i] = (float)(-log1p(-u_i)) for the first k of them (k <= V),
+ * and *first_zero = the first position i >= k whose uniform is 0 (its score
+ * p / q would be NaN on the host), else -1.  first_zero may be NULL. */
+int yuf_rng_exp_draws(yuf_rng *rng, int V, int k, float *q_out, int32_t *first_zero);
 
 #ifdef __cplusplus
 }

@@ -119,3 +119,24 @@ def test_native_generation_mask_rejects_bad_ids():
 def test_greedy_when_temperature_not_positive():
     x = np.array([0.1, 5.0, 2.0], np.float32)
     assert sample_token(x, 0.0, 0.95, Mt19937(1)) == 1
+
+
+@pytest.mark.parametrize("vocab,k", [(20480, 32), (300, 64), (40, 40), (7, 3)])
+def test_exp_draws_consume_what_a_sample_consumes(vocab, k):
+    """yuf_rng_exp_draws takes exactly the V uniforms of one host sample (the
+    generators agree afterwards) and its q are -log1p(-u) of torch's stream."""
+    rng_a, rng_b = Mt19937(5), Mt19937(5)
+    q, first_zero = rng_a.exp_draws(vocab, k)
+    sample_token(np.zeros(vocab, np.float32), 1.0, 0.9, rng_b, top_k=min(k, vocab))
+    assert [rng_a.next_u32() for _ in range(5)] == [rng_b.next_u32() for _ in range(5)]
+    torch.manual_seed(5)
+    u = torch.rand(vocab, dtype=torch.float64)
+    np.testing.assert_array_equal(q, (-torch.log1p(-u[:k])).to(torch.float32).numpy())
+    assert first_zero == -1
+
+
+def test_rng_copy_is_independent():
+    rng = Mt19937(11)
+    rng.next_u32()
+    twin = rng.copy()
+    assert [rng.next_u32() for _ in range(700)] == [twin.next_u32() for _ in range(700)]

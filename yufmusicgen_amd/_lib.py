@@ -80,6 +80,12 @@ SIGNATURES = {
     "yuf_argmax": (ctypes.c_int32, [c_void_p, ctypes.c_int]),
     "yuf_generation_mask": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_int, c_void_p, ctypes.c_int, c_void_p]),
+    "yuf_sample_device_masked": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_float, ctypes.c_float,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                c_void_p, c_void_p, ctypes.c_int, c_void_p, c_void_p, ctypes.c_uint64,
+                                                ctypes.c_uint64, c_void_p, c_void_p]),
+    "yuf_rng_exp_draws": (ctypes.c_int, [ctypes.POINTER(RngC), ctypes.c_int, ctypes.c_int, c_void_p,
+                                         ctypes.POINTER(ctypes.c_int32)]),
     "yuf_sample_device": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_float, ctypes.c_int,
                                          ctypes.c_uint64, ctypes.c_uint64, c_void_p, c_void_p]),
 }

@@ -84,7 +84,8 @@ struct GemmParams {
     const float *W = nullptr;
     int ldw = 0;
     // bf16 weights (raw bits, [N][ldw]) instead of W: the large-tile and decode
-    // kernels round A to bf16 and accumulate in fp32; needs K % 8 == 0.
+    // kernels split A into bf16 hi + lo parts and accumulate in fp32; needs
+    // K % 8 == 0.
     const uint16_t *Wh = nullptr;
     float *C = nullptr;
     int ldc = 0;
@@ -182,7 +183,29 @@ hipError_t launch_fill(float *p, size_t n, float value, hipStream_t stream);
 hipError_t launch_rosa_gates(float *x, int M, int D, int ld, hipStream_t stream);
 
 // -------------------------------------------------------------------- sampling
-hipError_t launch_sample(int n, int V, const float *logits, float temperature, int top_k,
-                         uint64_t seed, uint64_t counter, int32_t *tokens, hipStream_t stream);
+// One workgroup per stream (row of `logits`, [n, V]): optional generation
+// mask, temperature, top-k (1..64) and top-p, then the draw argmax p / q with
+// q = exp_draws[stream][position] (host MT19937 Exp(1) draws) or, when
+// exp_draws is null, -log u from a counter-based hash.
+constexpr int kSampleMaxBlocked = 256;  // blocked raw ids carried in the kernel arguments
+constexpr int kSampleMaskWords = 1024;  // blocked-id bitmap: raw ids below 32768
+struct SampleParams {
+    int V = 0;
+    const float *logits = nullptr;
+    float temperature = 1.0f, top_p = 1.0f;
+    int top_k = 0;
+    // Generation mask (midi_offset < 0: none).  The EOS id is allowed once the
+    // stream's index (index[s], or index_all when index is null) reaches
+    // min_before_eos.
+    int midi_offset = -1, eos_id = 0, min_before_eos = 0, index_all = 0;
+    const int32_t *index = nullptr;
+    int n_blocked = 0;
+    int blocked[kSampleMaxBlocked] = {};
+    const float *exp_draws = nullptr;     // [n, top_k]
+    const int32_t *first_zero = nullptr;  // [n]: first position >= top_k whose draw is 0, else -1
+    uint64_t seed = 0, counter = 0;
+    int32_t *tokens = nullptr;  // [n]
+};
+hipError_t launch_sample(const SampleParams &p, int n, hipStream_t stream);
 
 }  // namespace yuf

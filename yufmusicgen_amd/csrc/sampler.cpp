@@ -9,8 +9,11 @@
 //   torch.multinomial(p, 1): q ~ Exp(1) for every entry (53-bit uniforms from
 //   two MT19937 words, -log1p(-u) in double, cast to float), argmax(p / q).
 // The Gumbel/exponential stream is bit-identical to torch.manual_seed's; the
-// softmax exponentials come from libm, so a token can differ from torch only
-// when two candidates are tied to the last bit.
+// softmax exponentials are correctly rounded float exps (the double exp
+// rounded once), which torch's vectorised exp matches to within an ulp, so a
+// token can differ from torch only when two candidates are tied to the last
+// bit.  The device sampler's exact mode (yuf_sample_device_masked with host
+// draws) computes the same floats.
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -67,7 +70,7 @@ void softmax(const std::vector<float> &x, std::vector<float> &p) {
     float mx = -INFINITY;
     for (float v : x) mx = std::max(mx, v);
     p.resize(n);
-    for (size_t i = 0; i < n; ++i) p[i] = std::exp(x[i] - mx);
+    for (size_t i = 0; i < n; ++i) p[i] = (float)std::exp((double)(x[i] - mx));
     const float inv = 1.0f / vec_sum(p.data(), n);
     for (size_t i = 0; i < n; ++i) p[i] = p[i] * inv;
 }
@@ -97,6 +100,18 @@ extern "C" double yuf_rng_next_uniform(yuf_rng *r) {
     const uint64_t hi = yuf_rng_next_u32(r), lo = yuf_rng_next_u32(r);
     const uint64_t composite = (hi << 32) | lo;
     return (double)(composite & ((1ull << 53) - 1)) * (1.0 / (double)(1ull << 53));
+}
+
+extern "C" int yuf_rng_exp_draws(yuf_rng *r, int V, int k, float *q_out, int32_t *first_zero) {
+    if (!r || V <= 0 || k < 0 || (k > 0 && !q_out)) return yuf::fail(YUF_ERR_INVALID, "yuf_rng_exp_draws: bad arguments");
+    int32_t fz = -1;
+    for (int i = 0; i < V; ++i) {
+        const double u = yuf_rng_next_uniform(r);
+        if (i < k) q_out[i] = (float)(-std::log1p(-u));
+        else if (u == 0.0 && fz < 0) fz = i;
+    }
+    if (first_zero) *first_zero = fz;
+    return YUF_OK;
 }
 
 extern "C" int32_t yuf_argmax(const float *logits, int V) {

@@ -219,11 +219,28 @@ class Mt19937:
         self._rng = RngC()
         lib().yuf_rng_seed(ctypes.byref(self._rng), int(seed) & 0xFFFFFFFFFFFFFFFF)
 
+    def copy(self) -> "Mt19937":
+        """An independent generator in the same state."""
+        other = Mt19937.__new__(Mt19937)
+        other._rng = RngC()
+        ctypes.memmove(ctypes.byref(other._rng), ctypes.byref(self._rng), ctypes.sizeof(RngC))
+        return other
+
     def next_u32(self) -> int:
         return int(lib().yuf_rng_next_u32(ctypes.byref(self._rng)))
 
     def next_uniform(self) -> float:
         return float(lib().yuf_rng_next_uniform(ctypes.byref(self._rng)))
+
+    def exp_draws(self, vocab: int, k: int):
+        """The Exp(1) draws one host sample over ``vocab`` logits consumes:
+        (the first ``k`` as float32, the first later position whose uniform is
+        0 or -1) -- the device sampler's exact-mode input."""
+        q = np.empty(k, np.float32)
+        fz = ctypes.c_int32()
+        check(lib().yuf_rng_exp_draws(ctypes.byref(self._rng), int(vocab), int(k), q.ctypes.data if k else None,
+                                      ctypes.byref(fz)))
+        return q, int(fz.value)
 
 
 def sample_token(logits, temperature: float, top_p: float, rng: Mt19937, top_k: int = 0) -> int:
@@ -265,3 +282,30 @@ def sample_device(logits_dev, tokens_dev, temperature: float, top_k: int, seed: 
     st = torch.cuda.current_stream().cuda_stream if stream is None else stream
     check(lib().yuf_sample_device(n, vocab, logits_dev.data_ptr(), float(temperature), int(top_k), int(seed),
                                   int(counter), tokens_dev.data_ptr(), st))
+
+
+def sample_device_masked(logits_dev, tokens_dev, temperature: float, top_p: float, top_k: int, *,
+                         mask: dict | None = None, index=0, exp_draws=None, first_zero=None, seed: int = 0,
+                         counter: int = 0, stream=None) -> None:
+    """Generation mask + sampler of every row of ``logits_dev`` [n, V] on the GPU
+    (``yuf_sample_device_masked``).  ``mask``: dict(midi_offset=260, eos_id=2,
+    min_before_eos=16, blocked=(...)) or None; ``index``: an int for every
+    stream or an int32 GPU tensor [n]; ``exp_draws`` [n, top_k] float32 and
+    ``first_zero`` [n] int32 GPU tensors (from ``Mt19937.exp_draws``) select
+    the exact mode, else the counter-based draws of ``seed`` / ``counter``."""
+    import torch
+
+    n, vocab = logits_dev.shape
+    st = torch.cuda.current_stream().cuda_stream if stream is None else stream
+    mo, eos, mbe, blocked = -1, 2, 16, np.zeros(0, np.int32)
+    if mask is not None:
+        mo = int(mask.get("midi_offset", 260))
+        eos = int(mask.get("eos_id", 2))
+        mbe = int(mask.get("min_before_eos", 16))
+        blocked = np.ascontiguousarray(mask.get("blocked", ()), dtype=np.int32)
+    idx_host, idx_dev = (int(index), None) if isinstance(index, (int, np.integer)) else (0, index)
+    check(lib().yuf_sample_device_masked(
+        n, vocab, logits_dev.data_ptr(), float(temperature), float(top_p), int(top_k), mo, eos, mbe, idx_host,
+        None if idx_dev is None else idx_dev.data_ptr(), blocked.ctypes.data if blocked.size else None, blocked.size,
+        None if exp_draws is None else exp_draws.data_ptr(), None if first_zero is None else first_zero.data_ptr(),
+        int(seed), int(counter), tokens_dev.data_ptr(), st))
