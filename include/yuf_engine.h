@@ -95,6 +95,26 @@ int yuf_rosa_scan_f32(int B, int T, int D,
                       void *stream);
 
 /*
+ * yuf_rosa_scan_f32 without any allocation: no hipMalloc, hipFree or other
+ * allocating call.  No counterpart in the reference; for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  Same arguments, semantics and results.
+ * The segmented form (T % 64 == 0, T >= 128, D in {64, 128, 256}) keeps its
+ * scratch -- D * D + 3 * B * (T / 64) * D floats -- in a static 16 MiB device
+ * array (4,194,304 floats) that every GPU the library runs on holds until the
+ * process ends; larger calls fail with YUF_ERR_INVALID.  Other shapes use no
+ * scratch.  All calls on one GPU share that array: calls that overlap on one
+ * GPU (other streams, other host threads) race and must be ordered by the
+ * caller.  The first call on a device resolves the array's address there
+ * (hipGetSymbolAddress, not a stream operation).
+ */
+int yuf_rosa_scan_f32_noalloc(int B, int T, int D,
+                              const float *cand, const float *write, const float *read_raw,
+                              const float *decay, const float *direction,
+                              const float *memory_in, float *memory_out, float *read_out,
+                              void *stream);
+
+/*
  * Linear layer on the matrix cores: C = act(A W^T + bias) + residual, fp32.
  * The projection primitive of every nn.Linear on the path
  * (yufmusicgen/model.py:107-112, :196, :306-342, :377, :421).

@@ -32,3 +32,12 @@ def test_errors_cross_the_abi_as_status_codes():
     assert rc == -1 and "head size" in lib.yuf_last_error().decode()
     rc = lib.yuf_rosa_scan_f32(1, 1, 2048, *([None] * 9))
     assert rc == -1 and "D must be" in lib.yuf_last_error().decode()
+
+
+def test_noalloc_rosa_rejects_scratch_beyond_its_static_buffer():
+    """Checked on the host before any HIP call: B = 64, T = 8192, D = 256 needs
+    65536 + 3 * 64 * 128 * 256 floats, past the 4,194,304 of the buffer."""
+    lib = _lib.lib()
+    dummy = 256  # never dereferenced: the call returns before any device work
+    rc = lib.yuf_rosa_scan_f32_noalloc(64, 8192, 256, *([dummy] * 9))
+    assert rc == -1 and "static buffer" in lib.yuf_last_error().decode()

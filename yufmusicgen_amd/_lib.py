@@ -45,6 +45,7 @@ SIGNATURES = {
     "yuf_version": (ctypes.c_char_p, []),
     "yuf_wkv7_scan_f32": (ctypes.c_int, [ctypes.c_int] * 4 + [c_void_p] * 10),
     "yuf_rosa_scan_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
+    "yuf_rosa_scan_f32_noalloc": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_ln_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_linear_bf16w": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),

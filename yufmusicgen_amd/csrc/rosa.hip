@@ -576,10 +576,47 @@ hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
 
 }  // namespace yuf
 
-extern "C" int yuf_rosa_scan_f32(int B, int T, int D, const float *cand, const float *write,
-                                 const float *read_raw, const float *decay, const float *direction,
-                                 const float *memory_in, float *memory_out, float *read_out, void *stream) {
-    using namespace yuf;
+namespace yuf {
+namespace {
+
+// The no-allocation operator variant (yuf_rosa_scan_f32_noalloc) keeps the
+// segmented scan's scratch -- A^L and the z / carry / ends segment rows -- in
+// this file-scope device array: every device the library runs on holds one
+// copy, at its own address, until the process ends.  Nothing in it needs to
+// start at zero (each pass writes its rows before the next reads them).
+constexpr size_t kNoAllocScratchFloats = (size_t)4 << 20;  // 16 MiB
+__device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+// Device address of `scratch` per device, resolved once per device with that
+// device current (the array's name is a host-side stand-in, never passed to a
+// kernel).  Fixed storage: no host or device allocation on this path.
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+float *g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+int noalloc_scratch(float **out) {
+    int dev = 0;
+    hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("rosa noalloc: hipGetDevice: ") + hipGetErrorString(err));
+    if (dev < 0 || dev >= kNoAllocMaxDevices) return fail(YUF_ERR_INVALID, "rosa noalloc: device index above 63");
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *ptr = nullptr;
+        err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr)
+            return fail(YUF_ERR_HIP, std::string("rosa noalloc: hipGetSymbolAddress: ") + hipGetErrorString(err));
+        g_noalloc_ptr[dev] = static_cast<float *>(ptr);
+    }
+    *out = g_noalloc_ptr[dev];
+    return YUF_OK;
+}
+
+// The operator: argument checks, then the segmented form (scratch from the
+// growing per-stream buffer, or from `scratch` when noalloc) or the
+// sequential chunked scan (no scratch).
+int rosa_operator(int B, int T, int D, const float *cand, const float *write, const float *read_raw,
+                  const float *decay, const float *direction, const float *memory_in, float *memory_out,
+                  float *read_out, void *stream, bool noalloc) {
     if (B < 0 || T < 0) return fail(YUF_ERR_INVALID, "rosa: negative size");
     if (D < 1 || D > 1024) return fail(YUF_ERR_INVALID, "rosa: D must be in [1, 1024], got " + std::to_string(D));
     if (!decay || !direction) return fail(YUF_ERR_INVALID, "rosa: null decay/direction");
@@ -594,11 +631,21 @@ extern "C" int yuf_rosa_scan_f32(int B, int T, int D, const float *cand, const f
     if (B > 0 && rosa_segmented_ok(T, D, kOpRosaSeg) && !op_rosa_sequential()) {
         // Segmented form (as the engine's prefill): A^L on the device, then
         // segments from zero, the carry chain, and segments from their starts.
-        float *scratch = nullptr;
+        float *buf = nullptr;
         const size_t seg = (size_t)B * (T / kOpRosaSeg) * D;
-        if ((err = op_rosa_scratch(st, (size_t)D * D + 3 * seg, &scratch)) != hipSuccess)
+        const size_t need = (size_t)D * D + 3 * seg;
+        if (noalloc) {
+            if (need > kNoAllocScratchFloats)
+                return fail(YUF_ERR_INVALID, "rosa noalloc: B * (T / 64) * D = " + std::to_string(seg) +
+                                                 " needs " + std::to_string(need) + " scratch floats (D^2 + 3 B (T / 64) D); "
+                                                 "the static buffer holds " + std::to_string(kNoAllocScratchFloats) +
+                                                 " -- split the batch or use yuf_rosa_scan_f32");
+            int rc = noalloc_scratch(&buf);
+            if (rc != YUF_OK) return rc;
+        } else if ((err = op_rosa_scratch(st, need, &buf)) != hipSuccess) {
             return fail(YUF_ERR_OOM, std::string("rosa scratch: ") + hipGetErrorString(err));
-        float *AL = scratch, *z = AL + (size_t)D * D, *carry = z + seg, *ends = carry + seg;
+        }
+        float *AL = buf, *z = AL + (size_t)D * D, *carry = z + seg, *ends = carry + seg;
         err = launch_rosa_power(D, kOpRosaSeg, decay, direction, AL, st);
         if (err == hipSuccess) err = launch_rosa_segmented(p, AL, kOpRosaSeg, z, carry, ends, st);
     } else {
@@ -606,4 +653,21 @@ extern "C" int yuf_rosa_scan_f32(int B, int T, int D, const float *cand, const f
     }
     if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("rosa launch: ") + hipGetErrorString(err));
     return YUF_OK;
+}
+
+}  // namespace
+}  // namespace yuf
+
+extern "C" int yuf_rosa_scan_f32(int B, int T, int D, const float *cand, const float *write,
+                                 const float *read_raw, const float *decay, const float *direction,
+                                 const float *memory_in, float *memory_out, float *read_out, void *stream) {
+    return yuf::rosa_operator(B, T, D, cand, write, read_raw, decay, direction, memory_in, memory_out, read_out,
+                              stream, false);
+}
+
+extern "C" int yuf_rosa_scan_f32_noalloc(int B, int T, int D, const float *cand, const float *write,
+                                         const float *read_raw, const float *decay, const float *direction,
+                                         const float *memory_in, float *memory_out, float *read_out, void *stream) {
+    return yuf::rosa_operator(B, T, D, cand, write, read_raw, decay, direction, memory_in, memory_out, read_out,
+                              stream, true);
 }
