@@ -52,6 +52,9 @@
 #include "common.h"
 #include "kernels.h"
 
+#include <cstdlib>
+#include <cstring>
+
 namespace yuf {
 namespace {
 
@@ -77,8 +80,11 @@ __device__ __forceinline__ void buf_store4(floatx4 v, __amdgpu_buffer_rsrc_t rsr
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rsrc, byte_offset, 0, 0);
 }
 
-template <int NB>
+template <int NB, bool SPLIT>
 struct Lds {
+    // Ring depths: a split workgroup's Y wave reads chunk c - 1's ring entries
+    // while stage A writes chunk c + 3 and stage B1 chunk c + 2.
+    static constexpr int kRA = SPLIT ? 5 : 4, kRG = SPLIT ? 4 : 3;
     static constexpr int NP = 16 * NB;        // padded head size
     static constexpr int SA = NP + 4;         // row stride of [token][column] tiles
     // Ring A (4 chunks in flight): A~, R~ [16][SA]; B^^T, K^^T [NP][kST]; g_15 [NP];
@@ -95,14 +101,18 @@ struct Lds {
     // Stage A transpose (one region per stage-A wave): up to 5 inputs x
     // [16 tokens][16 columns], rows padded to kST floats.
     static constexpr int kSlotR = 5 * 16 * kST;
-    static constexpr int kFloats = 4 * kSlotA + 3 * kSlotG + 2 * kSlotT + 2 * kSlotN + NB * kSlotR;
+    // Split: consumer -> Y wave exchange, [chunk parity][value tile][vector k]
+    // [lane] floatx4: k < NB the chunk-start state S0^T rows, k = NB the U tile.
+    static constexpr int kSlotX = SPLIT ? 2 * 2 * 4 * 64 * 4 : 0;
+    static constexpr int kFloats =
+        kRA * kSlotA + kRG * kSlotG + 2 * kSlotT + 2 * kSlotN + NB * kSlotR + kSlotX;
 };
 
 // Wave roles.  Waves w and w + 4 of a workgroup share a SIMD, and a wave
 // issuing MFMAs halves the VALU issue rate of its SIMD neighbour, so each
 // MFMA-heavy wave (consumer or B1) is paired with one VALU-heavy wave
 // (stage A or B2): NB = 3 gives cons0+A0, cons1+A1, B1+B2, cons2+A2.
-enum : int { kRoleB1 = 8, kRoleB2 = 9, kRoleA = 12 };
+enum : int { kRoleB1 = 8, kRoleB2 = 9, kRoleIdle = 10, kRoleY = 11, kRoleA = 12 };
 template <int NB> struct Roles {
     static constexpr int kWaves = 2 * NB + 2;
     __device__ static int of(int w) {
@@ -114,26 +124,56 @@ template <int NB> struct Roles {
         return r[w];
     }
 };
+// Split heads (two workgroups per head, each with the consumers of its own
+// value tiles and the whole key-space pipeline, NB <= 3).  On gfx950 an fp32
+// MFMA stream and the VALU / LDS work of any wave on the same SIMD run one
+// after the other (measured: no overlap), so the work is spread for equal
+// per-SIMD sums: the consumers keep only the state chain (X, U, the state
+// update) and hand the chunk-start state and U to a Y wave that forms the
+// outputs one chunk later.  NB = 3: cons0 + A0, cons1 + A1, B1 + B2, Y + A2.
+// Consumer roles past the workgroup's tile count idle (they keep the barrier
+// count only).
+template <int NB> struct SplitRoles {
+    static constexpr int kWaves = NB == 2 ? 6 : 8;
+    __device__ static int of(int w) {
+        constexpr int A = kRoleA;
+        if constexpr (NB == 2) { constexpr int r[] = {0, kRoleB1, kRoleY, A, A + 1, kRoleB2}; return r[w]; }
+        constexpr int r[] = {0, 1, kRoleB1, kRoleY, A, A + 1, kRoleB2, A + 2};
+        return r[w];
+    }
+};
+template <int NB, bool SPLIT> struct RoleMap : Roles<NB> {};
+template <int NB> struct RoleMap<NB, true> : SplitRoles<NB> {
+    static_assert(NB == 2 || NB == 3, "split heads need NB in {2, 3}");
+};
 
-template <int NB, bool PREP>
-__global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
-    wkv7_chunk_kernel(WkvParams p, int N, int heads, int per_xcd) {
-    using Ly = Lds<NB>;
-    using Ro = Roles<NB>;
-    constexpr int NP = Ly::NP, SA = Ly::SA;
+// SPLIT: two workgroups per head; the first owns value tiles [0, (NB + 1) / 2),
+// the second the rest.
+template <int NB, bool PREP, bool SPLIT>
+__global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
+    wkv7_chunk_kernel(WkvParams p, int N, int units, int per_xcd) {
+    using Ly = Lds<NB, SPLIT>;
+    constexpr int NP = Ly::NP, SA = Ly::SA, kRA = Ly::kRA, kRG = Ly::kRG;
+    constexpr int kExtra = SPLIT ? 1 : 0;  // iterations after the consumers' last chunk (the Y wave's)
     __shared__ __attribute__((aligned(16))) float lds[Ly::kFloats];
     float *ringA = lds;
-    float *ringG = ringA + 4 * Ly::kSlotA;
-    float *ringT = ringG + 3 * Ly::kSlotG;
+    float *ringG = ringA + kRA * Ly::kSlotA;
+    float *ringT = ringG + kRG * Ly::kSlotG;
     float *ringN = ringT + 2 * Ly::kSlotT;
     float *stageR = ringN + 2 * Ly::kSlotN;
+    floatx4 *xch = reinterpret_cast<floatx4 *>(stageR + NB * Ly::kSlotR);  // split only
 
-    // XCD-aware head index: consecutive heads of a batch row share an XCD's L2.
-    const int flat = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
-    if (flat >= heads) return;  // uniform over the workgroup
+    // XCD-aware unit index: consecutive units (the two halves of a head, then
+    // consecutive heads of a batch row) share an XCD's L2.
+    const int unit = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (unit >= units) return;  // uniform over the workgroup
+    const int flat = SPLIT ? unit >> 1 : unit, part = SPLIT ? unit & 1 : 0;
+    constexpr int kNv0 = SPLIT ? (NB + 1) / 2 : NB;  // value tiles of the first workgroup
+    const int vb0 = part ? kNv0 : 0, nv = part ? NB - kNv0 : kNv0;
     const int bb = flat / p.H, h = flat - bb * p.H;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int role = Ro::of(wave);
+    int role = RoleMap<NB, SPLIT>::of(wave);
+    if (role < NB && role >= nv) role = kRoleIdle;
     const int g = lane >> 4, li = lane & 15;
     const int T = p.T, HN = p.H * N;
     const int n_chunks = (T + kC - 1) / kC;
@@ -145,9 +185,54 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
     const int slot = p.slot ? p.slot[bb] : bb;
     const size_t state_off = ((size_t)slot * p.H + h) * N * N;
 
-    if (role < NB) {
+    if (role == kRoleIdle) {
+        for (int it = -4; it < n_chunks + kExtra; ++it) lds_barrier();
+    } else if (SPLIT && role == kRoleY) {
+        // ------------------------------------------------------------ Y wave
+        // Chunk c = it - 1 of each owned value tile: Y = R~ S0^T + Qb U + Qk V
+        // from the consumer's exchange (S0^T, U), then the y rows.
+        const auto ry = make_rsrc(p.y + tok_base, tok_bytes);
+        for (int it = -4; it < n_chunks + kExtra; ++it) {
+            const int c = it - 1;
+            if (c >= 0) {
+                const float *sA = ringA + (c % kRA) * Ly::kSlotA;
+                const float *sG = ringG + (c % kRG) * Ly::kSlotG;
+                const floatx4 *xc = xch + (c & 1) * 2 * 4 * 64;
+                for (int tl = 0; tl < nv; ++tl) {
+                    const int i = 16 * (vb0 + tl) + li;
+                    const floatx4 *xt = xc + tl * 4 * 64;
+                    const floatx4 v = ld4(sA + Ly::oV + i * kST + 4 * g);
+                    const floatx4 U = xt[NB * 64 + lane];
+                    floatx4 Y0 = {0.f, 0.f, 0.f, 0.f}, Y1 = Y0;
+#pragma unroll
+                    for (int jb = 0; jb < NB; ++jb) {
+                        const floatx4 r4 = ld4(sA + Ly::oRs + li * SA + 16 * jb + 4 * g);
+                        const floatx4 s0 = xt[jb * 64 + lane];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            if (r & 1) Y1 = mfma(r4[r], s0[r], Y1);
+                            else Y0 = mfma(r4[r], s0[r], Y0);
+                        }
+                    }
+                    const floatx4 qk4 = ld4(sG + Ly::oQk + li * kST + 4 * g);
+                    const floatx4 qb4 = ld4(sG + Ly::oQb + li * kST + 4 * g);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        Y0 = mfma(qk4[r], v[r], Y0);
+                        Y1 = mfma(qb4[r], U[r], Y1);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int t = c * kC + 4 * g + r;
+                        buf_store(Y0[r] + Y1[r], ry, (t < T && i < N) ? (uint32_t)(t * HN + i) * 4u : kBufferOob);
+                    }
+                }
+            }
+            lds_barrier();
+        }
+    } else if (role < NB) {
         // ------------------------------------------------------------ consumer
-        const int q = role;
+        const int q = vb0 + role;
         const int i = 16 * q + li;  // value row owned by this lane's column of the tiles
         floatx4 S[NB];
         {
@@ -161,11 +246,55 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         }
         const auto ry = make_rsrc(p.y + tok_base, tok_bytes);
         wait_vmem();
-        for (int it = -4; it < n_chunks; ++it) {
-            if (it >= 0) {
+        for (int it = -4; it < n_chunks + kExtra; ++it) {
+            if (SPLIT && it >= 0 && it < n_chunks) {
+                // The state chain only: X = A~ S0^T + P V, U = (I - Gab)^{-1} X,
+                // S^T <- diag(g_15) (S^T + B^^T U + K^^T V); S0^T and U go to the Y wave.
                 const int c = it;
-                const float *sA = ringA + (c & 3) * Ly::kSlotA;
-                const float *sG = ringG + (c % 3) * Ly::kSlotG;
+                const float *sA = ringA + (c % kRA) * Ly::kSlotA;
+                const float *sG = ringG + (c % kRG) * Ly::kSlotG;
+                const float *sT = ringT + (c & 1) * Ly::kSlotT;
+                floatx4 *xt = xch + ((c & 1) * 2 + role) * 4 * 64;
+                const floatx4 v = ld4(sA + Ly::oV + i * kST + 4 * g);  // V[4 g + r][i]
+                floatx4 X0 = {0.f, 0.f, 0.f, 0.f}, X1 = X0;
+#pragma unroll
+                for (int jb = 0; jb < NB; ++jb) {
+                    const floatx4 a4 = ld4(sA + Ly::oAs + li * SA + 16 * jb + 4 * g);
+                    xt[jb * 64 + lane] = S[jb];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (r & 1) X1 = mfma(a4[r], S[jb][r], X1);
+                        else X0 = mfma(a4[r], S[jb][r], X0);
+                    }
+                }
+                const floatx4 p4 = ld4(sG + Ly::oP + li * kST + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (r & 1) X1 = mfma(p4[r], v[r], X1);
+                    else X0 = mfma(p4[r], v[r], X0);
+                }
+                const floatx4 X = X0 + X1;
+                const floatx4 ti4 = ld4(sT + li * kST + 4 * g);
+                floatx4 U = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) U = mfma(ti4[r], X[r], U);
+                xt[NB * 64 + lane] = U;
+#pragma unroll
+                for (int jb = 0; jb < NB; ++jb) {
+                    const floatx4 gl4 = ld4(sA + Ly::oGl + 16 * jb + 4 * g);
+                    const floatx4 bh4 = ld4(sA + Ly::oBhT + (16 * jb + li) * kST + 4 * g);
+                    const floatx4 kh4 = ld4(sA + Ly::oKhT + (16 * jb + li) * kST + 4 * g);
+                    floatx4 acc = S[jb];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc = mfma(bh4[r], U[r], acc);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc = mfma(kh4[r], v[r], acc);
+                    S[jb] = acc * gl4;
+                }
+            } else if (!SPLIT && it >= 0) {
+                const int c = it;
+                const float *sA = ringA + (c % kRA) * Ly::kSlotA;
+                const float *sG = ringG + (c % kRG) * Ly::kSlotG;
                 const float *sT = ringT + (c & 1) * Ly::kSlotT;
                 const floatx4 v = ld4(sA + Ly::oV + i * kST + 4 * g);  // V[4 g + r][i]
                 floatx4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
@@ -277,7 +406,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         // Chunk c (iteration c - 3); its set is reloaded with chunk c + 2.
         auto body = [&](int c, floatx4 (&ld)[kIn], bool load_next) {
             {
-                float *sA = ringA + (c & 3) * Ly::kSlotA;
+                float *sA = ringA + (c % kRA) * Ly::kSlotA;
                 transpose(ld);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) sA[Ly::oV + (lc0 + e) * kST + li] = ld[kT][e];
@@ -361,14 +490,14 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
         if (c < n_chunks) body(c, ld0, c + 2 < n_chunks);
         if (c + 1 < n_chunks) body(c + 1, ld1, false);
         if (c + 2 < n_chunks) body(c + 2, ld0, false);
-        for (int k = 0; k < 3; ++k) lds_barrier();
+        for (int k = 0; k < 3 + kExtra; ++k) lds_barrier();
     } else if (role == kRoleB1) {
         // ------------------------------------------------------------ stage B1
-        for (int it = -4; it < n_chunks; ++it) {
+        for (int it = -4; it < n_chunks + kExtra; ++it) {
             const int c = it + 2;
             if (c >= 0 && c < n_chunks) {
-                const float *sA = ringA + (c & 3) * Ly::kSlotA;
-                float *sG = ringG + (c % 3) * Ly::kSlotG;
+                const float *sA = ringA + (c % kRA) * Ly::kSlotA;
+                float *sG = ringG + (c % kRG) * Ly::kSlotG;
                 floatx4 gab = {0.f, 0.f, 0.f, 0.f}, gp = gab, gqb = gab, gqk = gab;
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
@@ -455,7 +584,7 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
             }
             const int c = it + 1;
             if (c >= 0 && c < n_chunks) {
-                const float *GT = ringG + (c % 3) * Ly::kSlotG + Ly::oGabT;
+                const float *GT = ringG + (c % kRG) * Ly::kSlotG + Ly::oGabT;
                 float *sT = ringT + (c & 1) * Ly::kSlotT;
                 // Column `lane` (< 16) of (I - Gab)^{-1}, right-looking: once x_s is
                 // final, x_t += Gab[t][s] x_s for every t > s.
@@ -491,19 +620,37 @@ __global__ void __launch_bounds__(Roles<NB>::kWaves * kWave)
             step(it, kraw0, it + 6 < n_chunks);
             if (it + 1 < n_chunks) step(it + 1, kraw1, it + 7 < n_chunks);
         }
+        for (int k = 0; k < kExtra; ++k) lds_barrier();
     }
+}
+
+// Heads at or below this many per GPU are split over two workgroups each (the
+// MI355X has 256 CUs; one workgroup per head would leave half of them idle).
+constexpr int kSplitMaxHeads = 128;
+
+template <int NB, bool SPLIT>
+hipError_t launch_nb_split(const WkvParams &p, int N, bool prep, hipStream_t stream) {
+    const int heads = p.B * p.H, units = SPLIT ? 2 * heads : heads;
+    const int per_xcd = (units + kXcds - 1) / kXcds;
+    const dim3 grid(per_xcd * kXcds), block(RoleMap<NB, SPLIT>::kWaves * kWave);
+    if (prep)
+        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, true, SPLIT>), grid, block, 0, stream, p, N, units, per_xcd);
+    else
+        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, false, SPLIT>), grid, block, 0, stream, p, N, units, per_xcd);
+    return hipGetLastError();
+}
+
+bool split_heads(int heads) {
+    if (const char *e = std::getenv("YUF_WKV7_SPLIT")) return std::strcmp(e, "0") != 0;
+    return heads <= kSplitMaxHeads;
 }
 
 template <int NB>
 hipError_t launch_nb(const WkvParams &p, int N, bool prep, hipStream_t stream) {
-    const int heads = p.B * p.H;
-    const int per_xcd = (heads + kXcds - 1) / kXcds;
-    const dim3 grid(per_xcd * kXcds), block(Roles<NB>::kWaves * kWave);
-    if (prep)
-        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, true>), grid, block, 0, stream, p, N, heads, per_xcd);
-    else
-        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, false>), grid, block, 0, stream, p, N, heads, per_xcd);
-    return hipGetLastError();
+    if constexpr (NB == 2 || NB == 3) {
+        if (split_heads(p.B * p.H)) return launch_nb_split<NB, true>(p, N, prep, stream);
+    }
+    return launch_nb_split<NB, false>(p, N, prep, stream);
 }
 
 }  // namespace
