@@ -99,3 +99,27 @@ def test_ln_linear_rejects_long_batches():
     with pytest.raises(YufError):
         check(lib().yuf_ln_linear_f32(65, 8, 64, A.data_ptr(), A.data_ptr(), A.data_ptr(), None, A.data_ptr(), None,
                                       None, A.data_ptr(), None))
+
+
+@pytest.mark.parametrize("m,n,k", [(16384, 5120, 640), (2048, 640, 2560), (512, 20480, 640), (300, 384, 64),
+                                   (1000, 160, 128), (256, 256, 32)])
+def test_large_tile_products_hold_fp32_accuracy(m, n, k):
+    """The large-tile path (M >= 256, K % 32 == 0) runs fp32 products as six bf16
+    MFMAs over three-part splits of both operands.  Element by element its error
+    against float64 must stay within what fp32 arithmetic itself allows: the
+    split and the dropped parts (<= 3 * 2^-24 of |a| |w| per term) plus the
+    fp32 accumulation of K terms (K * 2^-24 of sum |a| |w|, a worst-case
+    bound), i.e. <= (K + 3) 2^-24 (|A| |W|^T); a single bf16 rounding of either
+    operand (2^-9 relative) would break it by orders of magnitude."""
+    print(f"x3 linear {m}x{n}x{k}", flush=True)
+    rng = np.random.default_rng(m * 3 + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float32)
+    got = run_linear(a, w)
+    a64, w64 = a.astype(np.float64), w.astype(np.float64)
+    expect = a64 @ w64.T
+    mag = np.abs(a64) @ np.abs(w64).T
+    err = np.abs(got - expect)
+    assert np.all(err <= (k + 3) * 2.0 ** -24 * mag), float((err / mag).max())
+    # Typical error stays at fp32's level (relative to the magnitude sum).
+    assert float(np.median(err / mag)) < 4 * 2.0 ** -24

@@ -33,6 +33,8 @@
 // fp32 precision (a single bf16 rounding of A moves C5 logits by up to ~0.2
 // over 24 layers, against the configuration's 2e-2).  Needs K % 8 == 0.
 #include <algorithm>
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "common.h"
@@ -232,6 +234,21 @@ __device__ __forceinline__ bf16x8 to_bf16x8(floatx4 lo, floatx4 hi) {
     return r;
 }
 
+// The three bf16 parts of eight fp32 values: p1 = bf16(x), p2 = bf16(x - p1),
+// p3 = bf16(x - p1 - p2) (both differences exact in fp32); |x - p1 - p2 - p3|
+// <= 2^-24 |x| up to fp32 underflow.  Two values at a time: one packed
+// v_cvt_pk_bf16_f32 per part, shifts / masks back to fp32.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void split3_pair(floatx2 x, bf16x2 &p1, bf16x2 &p2, bf16x2 &p3) {
+    p1 = __builtin_convertvector(x, bf16x2);
+    const floatx2 r1 = x - __builtin_convertvector(p1, floatx2);
+    p2 = __builtin_convertvector(r1, bf16x2);
+    const floatx2 r2 = r1 - __builtin_convertvector(p2, floatx2);
+    p3 = __builtin_convertvector(r2, bf16x2);
+}
+
 // The two bf16 parts of eight fp32 values: hi = bf16(x), lo = bf16(x - hi).
 __device__ __forceinline__ void split_bf16x8(floatx4 x0, floatx4 x1, bf16x8 &hi, bf16x8 &lo) {
     hi = to_bf16x8(x0, x1);
@@ -339,11 +356,24 @@ __device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4
     return *reinterpret_cast<const float4 *>(stage + row * (WN + 4) + 4 * c4);
 }
 
-template <int BN, bool STAGED, bool WB>
+// X3 (fp32 A and W, K % 32 == 0): each staged fp32 value is split once, when
+// its tile is written to LDS, into three bf16 parts (split3_pair), kept as
+// three bf16 planes of A and of W in one LDS buffer (two barriers per K tile);
+// every 16 x 16 x 32 block then takes six v_mfma_f32_16x16x32_bf16 -- a3 w1,
+// a1 w3, a2 w2, a2 w1, a1 w2, a1 w1 (the terms below 2^-24 relative, a2 w3,
+// a3 w2 and a3 w3, are dropped) -- so the result is the fp32 product up to
+// about 3 * 2^-24 relative per term and fp32 accumulation order.  On gfx950
+// the bf16 matrix cores run a 32-k block in about 17 cycles against 256 for
+// eight 16 x 16 x 4 fp32 MFMAs.
+template <int BN, bool STAGED, bool WB, bool X3 = false>
 __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int per_xcd) {
+    static_assert(!(WB && X3), "X3 takes fp32 weights");
     constexpr int WN = BN / 2, NT = WN / 16;
-    constexpr int kBigBK = WB ? 32 : big_bk<BN>(), kBigLd = kBigBK + 4;
-    constexpr int kLdsFloats = WB ? (2 * (2 * kBigBM + BN) * kLdh) / 2 : 2 * (kBigBM + BN) * kBigLd;
+    constexpr int kBigBK = (WB || X3) ? 32 : big_bk<BN>(), kBigLd = kBigBK + 4;
+    // X3: one buffer of three bf16 planes each for A and W ([plane][row][kLdh]).
+    constexpr int kLdsFloats = WB   ? (2 * (2 * kBigBM + BN) * kLdh) / 2
+                               : X3 ? (3 * (kBigBM + BN) * kLdh) / 2
+                                    : 2 * (kBigBM + BN) * kBigLd;
     static_assert(kLdsFloats >= kBigThreads / 64 * 16 * (WN + 4), "LDS too small for the staged epilogue");
     __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
     float(*As)[kBigBM * kBigLd] = reinterpret_cast<float(*)[kBigBM * kBigLd]>(lds);
@@ -351,6 +381,8 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
     __bf16 *Ah = reinterpret_cast<__bf16 *>(lds);  // WB: A hi [2][kBigBM * kLdh], A lo [2][kBigBM * kLdh],
     __bf16 *Al = Ah + 2 * kBigBM * kLdh;            // then W [2][BN * kLdh]
     __bf16 *Bh = Al + 2 * kBigBM * kLdh;
+    __bf16 *Ap = reinterpret_cast<__bf16 *>(lds);  // X3: A planes [3][kBigBM * kLdh], then W planes [3][BN * kLdh]
+    __bf16 *Wp = Ap + 3 * kBigBM * kLdh;
 
     const GemmParams &p = g.p[blockIdx.y];
     const int tiles_n = g.tiles_n[blockIdx.y];
@@ -380,8 +412,29 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
         if constexpr (WB) big_load_h(tb, rw, p.ldw, k0, p.K, tid);
         else big_load(tb, rw, p.ldw, k0, p.K, tid);
     };
+    // X3: split each staged float4 into its three bf16 parts (one ds_write_b64 per plane).
+    auto store_planes = [&](const auto &t, __bf16 *dst, int plane_elems) {
+        using T = std::decay_t<decltype(t)>;
+#pragma unroll
+        for (int i = 0; i < T::kPer; ++i) {
+            const int q = tid + i * kBigThreads;
+            if (q < T::kF4) {
+                bf16x2 a0, b0, c0, a1, b1, c1;
+                split3_pair(floatx2{t.v[i].x, t.v[i].y}, a0, b0, c0);
+                split3_pair(floatx2{t.v[i].z, t.v[i].w}, a1, b1, c1);
+                __bf16 *o = dst + (q / 8) * kLdh + (q % 8) * 4;
+                typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+                *reinterpret_cast<bf16x4 *>(o) = __builtin_shufflevector(a0, a1, 0, 1, 2, 3);
+                *reinterpret_cast<bf16x4 *>(o + plane_elems) = __builtin_shufflevector(b0, b1, 0, 1, 2, 3);
+                *reinterpret_cast<bf16x4 *>(o + 2 * plane_elems) = __builtin_shufflevector(c0, c1, 0, 1, 2, 3);
+            }
+        }
+    };
     auto store_tiles = [&](int buf) {
-        if constexpr (WB) {
+        if constexpr (X3) {
+            store_planes(ta, Ap, kBigBM * kLdh);
+            store_planes(tb, Wp, BN * kLdh);
+        } else if constexpr (WB) {
             big_store_a_h(ta, Ah + buf * kBigBM * kLdh, Al + buf * kBigBM * kLdh, tid);
             big_store_h(tb, Bh + buf * BN * kLdh, tid);
         } else {
@@ -395,7 +448,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
     lds_barrier();
 
     for (int kt = 0; kt < k_tiles; ++kt) {
-        const int cur = kt & 1;
+        const int cur = X3 ? 0 : kt & 1;
         const bool more = kt + 1 < k_tiles;
         if (more) {
             big_load(ta, ra, p.lda, (kt + 1) * kBigBK, p.K, tid);
@@ -420,8 +473,51 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[i], bf[j], acc[i][j], 0, 0, 0);
                 }
         }
+        if constexpr (X3) {
+            // One 32-k step from the split planes: a lane's 8 consecutive k of a
+            // row are one ds_read_b128 per plane.
+            constexpr int PA = kBigBM * kLdh, PW = BN * kLdh;
+            bf16x8 a1[4], a2[4], a3[4];
 #pragma unroll
-        for (int h = 0; h < (WB ? 0 : kBigBK / 16); ++h) {  // 16 k per half: one ds_read_b128 per operand fragment
+            for (int i = 0; i < 4; ++i) {
+                const __bf16 *ap = Ap + (wm * 64 + i * 16 + li) * kLdh + 8 * g4;
+                a1[i] = *reinterpret_cast<const bf16x8 *>(ap);
+                a2[i] = *reinterpret_cast<const bf16x8 *>(ap + PA);
+                a3[i] = *reinterpret_cast<const bf16x8 *>(ap + 2 * PA);
+            }
+            // W fragments one ahead of their MFMAs, so the LDS latency of
+            // fragment j + 1 overlaps the products of fragment j.
+            const __bf16 *bp0 = Wp + (wn * WN + li) * kLdh + 8 * g4;
+            bf16x8 nw1 = *reinterpret_cast<const bf16x8 *>(bp0);
+            bf16x8 nw2 = *reinterpret_cast<const bf16x8 *>(bp0 + PW);
+            bf16x8 nw3 = *reinterpret_cast<const bf16x8 *>(bp0 + 2 * PW);
+            __builtin_amdgcn_sched_group_barrier(0x100, 15, 0);  // A fragments and W fragment 0 first
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const bf16x8 w1 = nw1, w2 = nw2, w3 = nw3;
+                if (j + 1 < NT) {
+                    const __bf16 *bp = bp0 + (j + 1) * 16 * kLdh;
+                    nw1 = *reinterpret_cast<const bf16x8 *>(bp);
+                    nw2 = *reinterpret_cast<const bf16x8 *>(bp + PW);
+                    nw3 = *reinterpret_cast<const bf16x8 *>(bp + 2 * PW);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    floatx4 c = acc[i][j];
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[i], w1, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w3, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[i], w2, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[i], w1, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w2, c, 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w1, c, 0, 0, 0);
+                }
+                // Keep the next fragment's reads ahead of this fragment's products.
+                if (j + 1 < NT) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // DS reads
+                __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);                 // MFMA
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < ((WB || X3) ? 0 : kBigBK / 16); ++h) {  // 16 k per half: one ds_read_b128 per operand fragment
             floatx4 af[4], bf[NT];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -437,7 +533,15 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
                     for (int j = 0; j < NT; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][r], bf[j][r], acc[i][j], 0, 0, 0);
         }
-        if (more) store_tiles(cur ^ 1);
+        if constexpr (X3) {
+            // One buffer: every wave is done with this tile before it is replaced.
+            if (more) {
+                lds_barrier();
+                store_tiles(0);
+            }
+        } else if (more) {
+            store_tiles(cur ^ 1);
+        }
         lds_barrier();
     }
 
@@ -1307,12 +1411,26 @@ __global__ void gemm_splitk_reduce_kernel(GemmParams p, int splits) {
     }
 }
 
-template <int BN, bool WB>
+template <int BN, bool WB, bool X3 = false>
 void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStream_t stream) {
     if (staged)
-        hipLaunchKernelGGL((gemm_big_kernel<BN, true, WB>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+        hipLaunchKernelGGL((gemm_big_kernel<BN, true, WB, X3>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
     else
-        hipLaunchKernelGGL((gemm_big_kernel<BN, false, WB>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+        hipLaunchKernelGGL((gemm_big_kernel<BN, false, WB, X3>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+}
+
+// fp32 products on the bf16 matrix cores through three-part splits (the X3
+// form of gemm_big_kernel) when every K of the group is a multiple of 32;
+// YUF_GEMM_X3=0 keeps the fp32 MFMA form.
+bool use_x3(const GemmGroup &g, int n) {
+    static const bool enabled = [] {
+        const char *e = std::getenv("YUF_GEMM_X3");
+        return !(e && std::strcmp(e, "0") == 0);
+    }();
+    if (!enabled) return false;
+    for (int i = 0; i < n; ++i)
+        if (g.p[i].K % 32 != 0) return false;
+    return true;
 }
 
 template <int NT, int MI, int PRO, bool WB, int S>
@@ -1620,7 +1738,16 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
             staged = staged && (bits & 15) == 0 && p.ldc % 4 == 0 && (!p.residual || p.ldr % 4 == 0);
         }
         const dim3 grid(per_xcd * kXcds, n), block(kBigThreads);
-switch (bn) {
+        if (use_x3(g, n)) {
+            switch (bn) {
+                case 256: launch_big<256, false, true>(g, per_xcd, staged, grid, stream); break;
+                case 160: launch_big<160, false, true>(g, per_xcd, staged, grid, stream); break;
+                case 128: launch_big<128, false, true>(g, per_xcd, staged, grid, stream); break;
+                default: launch_big<64, false, true>(g, per_xcd, staged, grid, stream); break;
+            }
+            return hipGetLastError();
+        }
+        switch (bn) {
             case 256: launch_big<256, false>(g, per_xcd, staged, grid, stream); break;
             case 160: launch_big<160, false>(g, per_xcd, staged, grid, stream); break;
             case 128: launch_big<128, false>(g, per_xcd, staged, grid, stream); break;
