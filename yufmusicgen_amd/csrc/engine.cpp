@@ -63,12 +63,22 @@ struct Engine {
     ModelShape s;
     int max_streams = 0, max_tokens = 0;
     hipStream_t stream = nullptr;
-    DeviceBuf weights, weights_h, state, work, io;
+    DeviceBuf weights, weights_h, weights_t, state, work, io;
     // bf16 mode: a bf16 image of the weight buffer (same element offsets); the
     // GEMMs of weights inside [w_base, w_base + w_floats) read it instead.
     const float *w_base = nullptr;
     size_t w_floats = 0;
     const uint16_t *w_h = nullptr;
+    // The projection matrices again in 16-row tiles for the decode kernels
+    // (GemmParams::Wt / Wht): fp32 16 x 16 tiles, or bf16 16 x 32 tiles in
+    // bf16 mode.  `base` is the row-major matrix in the weight buffer.
+    struct Tiled {
+        const float *base;
+        long long rows, cols;
+        const void *tiles;
+        int wt_ld;  // elements per row tile
+    };
+    std::vector<Tiled> tiled;
     std::vector<LayerW> layers;
     const float *emb = nullptr, *ln_fin_w = nullptr, *ln_fin_b = nullptr, *head = nullptr;
     // state arrays, [layer][slot][...]
@@ -305,6 +315,21 @@ GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, co
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = ldr; p.silu_pair = silu_pair;
     p.workspace = e.gemm_ws; p.workspace_floats = e.gemm_ws_floats;
     if (e.w_h && W >= e.w_base && W < e.w_base + e.w_floats) p.Wh = e.w_h + (W - e.w_base);
+    if (M <= 64) {
+        // Decode shapes: the tiled copy, when W is a tile-aligned block of a tiled matrix.
+        for (const Engine::Tiled &t : e.tiled) {
+            if (W < t.base || W >= t.base + t.rows * t.cols || ldw != t.cols) continue;
+            const long long off = W - t.base, r0 = off / t.cols, c0 = off % t.cols;
+            const int kt = e.w_h ? 32 : 16;
+            if (r0 % 16 == 0 && c0 % kt == 0) {
+                const size_t first = (size_t)(r0 / 16) * t.wt_ld + (size_t)(c0 / kt) * 16 * kt;
+                if (e.w_h) p.Wht = static_cast<const uint16_t *>(t.tiles) + first;
+                else p.Wt = static_cast<const float *>(t.tiles) + first;
+                p.wt_ld = t.wt_ld;
+            }
+            break;
+        }
+    }
     return p;
 }
 
@@ -795,6 +820,55 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
         w.ln_f_w = nxt(); w.ln_f_b = nxt(); w.ffn_cat = nxt(); w.ffn_out = nxt();
         w.rosa_al = nxt();
         w.rosa_u = nxt(); w.rosa_lam = nxt();
+    }
+    {
+        // Tiled copies of the decode products' matrices (from the host image).
+        const long long d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4LL * s.d;
+        std::vector<Engine::Tiled> mats;
+        mats.push_back({e.head, V, d, nullptr, 0});
+        for (const LayerW &w : e.layers) {
+            for (const float *m : {w.w_r, w.w_k, w.w_v, w.w_o}) mats.push_back({m, d, d, nullptr, 0});
+            for (const float *m : {w.w1t, w.a1t, w.g1t}) mats.push_back({m, L, d, nullptr, 0});
+            for (const float *m : {w.w2t, w.a2t, w.g2t}) mats.push_back({m, d, L, nullptr, 0});
+            mats.push_back({w.rosa_w3, 3 * D, d, nullptr, 0});
+            mats.push_back({w.rosa_out, d, D, nullptr, 0});
+            mats.push_back({w.ffn_cat, 2 * hid, d, nullptr, 0});
+            mats.push_back({w.ffn_out, d, hid, nullptr, 0});
+        }
+        const bool bf16 = e.w_h != nullptr;
+        const int kt = bf16 ? 32 : 16, esz = bf16 ? 2 : 4;
+        size_t total = 0;
+        std::vector<size_t> at;
+        for (Engine::Tiled &t : mats) {
+            t.wt_ld = (int)(((t.cols + kt - 1) / kt) * 16 * kt);
+            at.push_back(total);
+            total += (((size_t)((t.rows + 15) / 16) * t.wt_ld * esz + 255) / 256) * 256 / esz;
+        }
+        std::vector<uint16_t> th;
+        std::vector<float> tf;
+        try {
+            if (bf16) th.assign(total, 0);
+            else tf.assign(total, 0.0f);
+        } catch (const std::bad_alloc &) {
+            return fail(YUF_ERR_OOM, "out of host memory preparing tiled weights");
+        }
+        for (size_t i = 0; i < mats.size(); ++i) {
+            const Engine::Tiled &t = mats[i];
+            const float *src = host.data() + (t.base - base);
+            for (long long r = 0; r < t.rows; ++r)
+                for (long long c = 0; c < t.cols; ++c) {
+                    const size_t o = at[i] + (size_t)(r / 16) * t.wt_ld + (size_t)(c / kt) * 16 * kt + (r % 16) * kt + c % kt;
+                    if (bf16) th[o] = bf16_bits(src[r * t.cols + c]);
+                    else tf[o] = src[r * t.cols + c];
+                }
+        }
+        ENG_TRY(hipMalloc(&e.weights_t.p, total * esz), "tiled weights alloc");
+        ENG_TRY(hipMemcpy(e.weights_t.p, bf16 ? (const void *)th.data() : (const void *)tf.data(), total * esz,
+                          hipMemcpyHostToDevice),
+                "tiled weights upload");
+        for (size_t i = 0; i < mats.size(); ++i)
+            mats[i].tiles = static_cast<const char *>(e.weights_t.p) + at[i] * esz;
+        e.tiled = std::move(mats);
     }
 
     // State: [layer][slot][...] for each of prev, wkv, rosa.

@@ -735,8 +735,12 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
     const int spw = ((p.K + KS - 1) / KS + kDecWaves - 1) / kDecWaves;  // k steps per wave
     const int k_begin = min(p.K, wave * spw * KS), k_end = min(p.K, k_begin + spw * KS);
     const auto ra = make_rsrc(p.A + (size_t)row0 * p.lda, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
-    const auto rw = WB ? make_rsrc(p.Wh, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 2))
-                       : make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 4));
+    // Tiled W when given (contiguous 1 KB per wave load), else row-major W.
+    const bool tiled = WB ? p.Wht != nullptr : p.Wt != nullptr;
+    const uint32_t tiles_bytes = (uint32_t)((size_t)((p.N + 15) / 16) * p.wt_ld * (WB ? 2 : 4));
+    const auto rw = tiled ? make_rsrc(WB ? (const void *)p.Wht : (const void *)p.Wt, tiles_bytes)
+                  : WB    ? make_rsrc(p.Wh, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 2))
+                          : make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + p.K) * 4));
 
     floatx4 acc[NT][MI];
 #pragma unroll
@@ -756,7 +760,9 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int wr = w_row0 + 32 * t + li;
-            b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)((size_t)wr * p.ldw + k) * (WB ? 2u : 4u) : kBufferOob);
+            const size_t e = tiled ? (size_t)(wr >> 4) * p.wt_ld + (size_t)(k / KS) * (16 * KS) + (wr & 15) * KS + (k % KS)
+                                   : (size_t)wr * p.ldw + k;
+            b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)e * (WB ? 2u : 4u) : kBufferOob);
         }
     };
     auto load_a = [&](int s, int k0) {
@@ -1003,7 +1009,9 @@ __global__ void __launch_bounds__(kDecThreads) gemm_wide_kernel(GemmParams p, in
     const int g4 = lane >> 4, li = lane & 15;
     const int K = p.K, M = p.M, k0 = wave * 16 * S;
     const auto ra = make_rsrc(p.A, (uint32_t)(((size_t)(M - 1) * p.lda + K) * 4));
-    const auto rw = make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + K) * 4));
+    const bool tiled = p.Wt != nullptr;  // 16 x 16 tiles: one contiguous 1 KB run per wave load
+    const auto rw = tiled ? make_rsrc(p.Wt, (uint32_t)((size_t)((p.N + 15) / 16) * p.wt_ld * 4))
+                          : make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + K) * 4));
     auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
@@ -1021,7 +1029,9 @@ __global__ void __launch_bounds__(kDecThreads) gemm_wide_kernel(GemmParams p, in
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int k = k0 + 16 * s + 4 * g4;
-            b[s] = load4(rw, slice < slices && wr < p.N && k < K ? (uint32_t)((size_t)wr * p.ldw + k) * 4u : kBufferOob);
+            const size_t e = tiled ? (size_t)slice * p.wt_ld + (size_t)(k >> 4) * 256 + li * 16 + (k & 15)
+                                   : (size_t)wr * p.ldw + k;
+            b[s] = load4(rw, slice < slices && wr < p.N && k < K ? (uint32_t)e * 4u : kBufferOob);
         }
     };
     int j = blockIdx.x;

@@ -107,6 +107,14 @@ struct GemmParams {
     const float *ln_beta = nullptr;
     const float *a_gate = nullptr;
     int ldg = 0;
+    // Optional copy of W for the decode kernels (M <= 64) in 16-row tiles: row
+    // tile rt, k tile kt (16 k for fp32, 32 k for bf16) at rt * wt_ld + kt *
+    // 256 (fp32, 16 x 16 row-major) or kt * 512 (bf16, 16 x 32) elements, so
+    // the 16 rows x 16 k (32 k) a wave reads per k step are one contiguous
+    // 1 KB run -- about 4x the vector-load issue rate of 16 rows x 64 bytes.
+    const float *Wt = nullptr;
+    const uint16_t *Wht = nullptr;
+    int wt_ld = 0;
 };
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
 
