@@ -307,6 +307,21 @@ T *carve(char *&cursor, size_t count) {
     return p;
 }
 
+// The tiled copy of W (a tile-aligned block of one of e.tiled's matrices, row
+// stride ldw) for the decode kernels, or nullptr; *wt_ld receives its row-tile
+// stride.
+const void *tiled_copy(const Engine &e, const float *W, int ldw, int *wt_ld) {
+    for (const Engine::Tiled &t : e.tiled) {
+        if (W < t.base || W >= t.base + t.rows * t.cols || ldw != t.cols) continue;
+        const long long off = W - t.base, r0 = off / t.cols, c0 = off % t.cols;
+        const int kt = e.w_h ? 32 : 16, esz = e.w_h ? 2 : 4;
+        if (r0 % 16 != 0 || c0 % kt != 0) return nullptr;
+        *wt_ld = t.wt_ld;
+        return static_cast<const char *>(t.tiles) + ((size_t)(r0 / 16) * t.wt_ld + (size_t)(c0 / kt) * 16 * kt) * esz;
+    }
+    return nullptr;
+}
+
 GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C,
                      int ldc, const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr,
                      int ldr = 0, bool silu_pair = false) {
@@ -316,19 +331,9 @@ GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, co
     p.workspace = e.gemm_ws; p.workspace_floats = e.gemm_ws_floats;
     if (e.w_h && W >= e.w_base && W < e.w_base + e.w_floats) p.Wh = e.w_h + (W - e.w_base);
     if (M <= 64) {
-        // Decode shapes: the tiled copy, when W is a tile-aligned block of a tiled matrix.
-        for (const Engine::Tiled &t : e.tiled) {
-            if (W < t.base || W >= t.base + t.rows * t.cols || ldw != t.cols) continue;
-            const long long off = W - t.base, r0 = off / t.cols, c0 = off % t.cols;
-            const int kt = e.w_h ? 32 : 16;
-            if (r0 % 16 == 0 && c0 % kt == 0) {
-                const size_t first = (size_t)(r0 / 16) * t.wt_ld + (size_t)(c0 / kt) * 16 * kt;
-                if (e.w_h) p.Wht = static_cast<const uint16_t *>(t.tiles) + first;
-                else p.Wt = static_cast<const float *>(t.tiles) + first;
-                p.wt_ld = t.wt_ld;
-            }
-            break;
-        }
+        const void *t = tiled_copy(e, W, ldw, &p.wt_ld);
+        if (e.w_h) p.Wht = static_cast<const uint16_t *>(t);
+        else p.Wt = static_cast<const float *>(t);
     }
     return p;
 }
@@ -504,6 +509,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
             ro.pre = a.rosa3; ro.ld_pre = 3 * D;
             ro.mem = ros; ro.mem_rows = e.max_streams; ro.slot = a.slots;
             ro.u = w.rosa_u; ro.lam = w.rosa_lam; ro.W = w.rosa_out;
+            if (!e.w_h) ro.Wt = static_cast<const float *>(tiled_copy(e, w.rosa_out, D, &ro.wt_ld));
             ro.residual = a.h; ro.ldr = d; ro.C = a.h; ro.ldc = d;
             ro.counter = a.rcount;
             ENG_TRY(launch_rosa_out_decode(ro, st), "rosa out (fused step)");

@@ -1172,7 +1172,9 @@ __global__ void __launch_bounds__(kDecThreads) rosa_out_decode_kernel(RosaOutPar
     const auto rm = make_rsrc(p.mem, (uint32_t)((size_t)p.mem_rows * D * 4));
     const auto rp = make_rsrc(p.pre + (size_t)row0 * p.ld_pre, (uint32_t)(((size_t)(rows - 1) * p.ld_pre + 3 * D) * 4));
     const auto ru = make_rsrc(p.u, (uint32_t)D * 4u), rl = make_rsrc(p.lam, (uint32_t)D * 4u);
-    const auto rw = make_rsrc(p.W, (uint32_t)((size_t)p.N * D * 4));
+    const bool tiled = p.Wt != nullptr;  // one contiguous 1 KB run per wave load
+    const auto rw = tiled ? make_rsrc(p.Wt, (uint32_t)((size_t)((p.N + 15) / 16) * p.wt_ld * 4))
+                          : make_rsrc(p.W, (uint32_t)((size_t)p.N * D * 4));
     auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
@@ -1181,7 +1183,8 @@ __global__ void __launch_bounds__(kDecThreads) rosa_out_decode_kernel(RosaOutPar
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int k = kw + 16 * s + 4 * g4;
-        b[s] = load4(rw, wr < p.N ? (uint32_t)((size_t)wr * D + k) * 4u : kBufferOob);
+        const size_t we = tiled ? (size_t)slice * p.wt_ld + (size_t)(k >> 4) * 256 + li * 16 + (k & 15) : (size_t)wr * D + k;
+        b[s] = load4(rw, wr < p.N ? (uint32_t)we * 4u : kBufferOob);
         m[s] = load4(rm, rv ? (uint32_t)((size_t)slot * D + k) * 4u : kBufferOob);
         e[s] = load4(rp, rv ? (uint32_t)((size_t)li * p.ld_pre + k) * 4u : kBufferOob);
         gw[s] = load4(rp, rv ? (uint32_t)((size_t)li * p.ld_pre + D + k) * 4u : kBufferOob);

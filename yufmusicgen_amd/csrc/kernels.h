@@ -136,6 +136,8 @@ struct RosaOutParams {
     const int *slot = nullptr;
     const float *u = nullptr, *lam = nullptr;  // unit direction, sigmoid(decay) [D]
     const float *W = nullptr;
+    const float *Wt = nullptr;  // optional 16 x 16-tiled W (GemmParams::Wt layout), wt_ld floats per row tile
+    int wt_ld = 0;
     const float *bias = nullptr;
     const float *residual = nullptr;
     int ldr = 0;
