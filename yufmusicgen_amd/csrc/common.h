@@ -127,6 +127,13 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------
 constexpr uint32_t kBufferOob = 0x80000000u;  // an offset past any range used here
 
+// Decode activations in 16 x 16 tiles: element (r, c) of a [rows][ld] matrix at
+// [r / 16][c / 16][r % 16][c % 16] (row-tile stride 16 ld floats), so the 16
+// rows x 16 columns a wave reads per k step are one contiguous 1 KB run.
+__host__ __device__ __forceinline__ size_t tile_index(int r, int c, int ld) {
+    return (size_t)(r >> 4) * 16 * ld + (size_t)(c >> 4) * 256 + (r & 15) * 16 + (c & 15);
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, bytes, 0x00020000);
 }

@@ -68,7 +68,7 @@ __global__ void __launch_bounds__(256) ln_shift_kernel(float *__restrict__ x, in
                                                        const int *__restrict__ slot, const float *__restrict__ mix6,
                                                        float *__restrict__ out6, size_t out_stride,
                                                        const float *__restrict__ parts, size_t part_stride,
-                                                       int nparts) {
+                                                       int nparts, bool out_tiled) {
     __shared__ float part[2][4];
     const int row = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     float *xr = x + (size_t)row * d;
@@ -131,8 +131,9 @@ __global__ void __launch_bounds__(256) ln_shift_kernel(float *__restrict__ x, in
         if (c < d) {
             const float xv = (v[e] - mean) * rstd * gm[e] + bt[e];
             const float delta = xv - pv[e];
+            const size_t o = out_tiled ? tile_index(row, c, d) : (size_t)row * d + c;
 #pragma unroll
-            for (int q = 0; q < 6; ++q) out6[q * out_stride + (size_t)row * d + c] = fmaf(delta, mx[q][e], xv);
+            for (int q = 0; q < 6; ++q) out6[q * out_stride + o] = fmaf(delta, mx[q][e], xv);
             prow[c] = xv;
         }
     }
@@ -318,15 +319,16 @@ hipError_t launch_layernorm(const float *x, int M, int d, const float *gamma, co
 
 hipError_t launch_ln_shift(float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
                            const int *slot, const float *mix6, float *out6, size_t out_stride, const float *parts,
-                           size_t part_stride, int nparts, hipStream_t stream) {
+                           size_t part_stride, int nparts, bool out_tiled, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
     if (nparts < 0 || nparts > kMaxParts || (nparts > 0 && !parts)) return hipErrorInvalidValue;
+    if (out_tiled && (d % 16 != 0 || out_stride < (size_t)((n + 15) / 16) * 16 * d)) return hipErrorInvalidValue;
     const dim3 grid(n), block(256);
     const int per = (d + 255) / 256;
-    if (per <= 1) hipLaunchKernelGGL(ln_shift_kernel<1>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
-    else if (per <= 2) hipLaunchKernelGGL(ln_shift_kernel<2>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
-    else if (per <= 3) hipLaunchKernelGGL(ln_shift_kernel<3>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
-    else if (per <= 4) hipLaunchKernelGGL(ln_shift_kernel<4>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts);
+    if (per <= 1) hipLaunchKernelGGL(ln_shift_kernel<1>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts, out_tiled);
+    else if (per <= 2) hipLaunchKernelGGL(ln_shift_kernel<2>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts, out_tiled);
+    else if (per <= 3) hipLaunchKernelGGL(ln_shift_kernel<3>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts, out_tiled);
+    else if (per <= 4) hipLaunchKernelGGL(ln_shift_kernel<4>, grid, block, 0, stream, x, d, gamma, beta, prev_state, slot, mix6, out6, out_stride, parts, part_stride, nparts, out_tiled);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }

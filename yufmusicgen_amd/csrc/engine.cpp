@@ -91,6 +91,7 @@ struct Engine {
     float *kpart = nullptr;  // [kFfnParts][max_streams][d]: K-split partials of the decode FFN output
     bool rosa_segmented = true;                                // YUF_ROSA_SEGMENTED=0 disables
     bool decode_fusion = true;                                 // YUF_DECODE_FUSION=0: separate low-rank GEMM and ROSA step
+    bool act_tiles = true;                                     // YUF_DECODE_TILES=0: row-major decode activations
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
     size_t gemm_ws_floats = 0;
     // Out-of-range token flags set by the embedding kernel: bad_host for the
@@ -352,14 +353,17 @@ int gemm(Engine &e, hipStream_t st, int M, int N, int K, const float *A, int lda
 // through `scratch` first.
 int ln_gemm(Engine &e, hipStream_t st, int M, int N, int K, const float *A, int lda, const float *gamma,
             const float *beta, const float *gate, float *scratch, const float *W, float *C, int ldc,
-            const float *bias = nullptr, const float *residual = nullptr, int ldr = 0, bool silu_pair = false) {
+            const float *bias = nullptr, const float *residual = nullptr, int ldr = 0, bool silu_pair = false,
+            bool a_tiled = false, bool c_tiled = false) {
     // Wide N fuses only where the wide decode kernel runs (fp32 W, 32 < M, K <= 640).
     if (M <= 64 && K % 4 == 0 && K <= 1024 && (N <= 8192 || (M > 32 && K <= 640 && !e.w_h))) {
         GemmParams p = make_gemm(e, M, N, K, A, lda, W, K, C, ldc, bias, ACT_NONE, residual, ldr, silu_pair);
         p.ln_gamma = gamma; p.ln_beta = beta; p.a_gate = gate; p.ldg = gate ? lda : 0;
+        p.a_tiled = a_tiled; p.c_tiled = c_tiled;
         ENG_TRY(launch_gemm(p, st), "ln gemm");
         return YUF_OK;
     }
+    if (a_tiled || c_tiled) return fail(YUF_ERR_INVALID, "ln_gemm: tiled operands need the fused path");
     if (lda != K) return fail(YUF_ERR_INVALID, "ln_gemm: strided rows need the fused path");
     ENG_TRY(launch_layernorm(A, M, K, gamma, beta, gate, scratch, st), "layernorm");
     return gemm(e, st, M, N, K, scratch, K, W, K, C, ldc, bias, ACT_NONE, residual, ldr, silu_pair);
@@ -385,6 +389,7 @@ struct Act {
     int *rcount;  // fused ROSA-out tile counters of this group of streams
     float *kpart;  // FFN-out K-split partials of these streams, planes kplane floats apart
     size_t kplane;
+    bool tile_aligned;  // the rows start at a multiple of 16 (16 x 16-tiled decode activations possible)
 };
 
 Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
@@ -407,6 +412,7 @@ Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
     a.rcount = e.rosa_count + s0;
     a.kpart = e.kpart + (size_t)s0 * d;
     a.kplane = (size_t)e.max_streams * d;
+    a.tile_aligned = m0 % 16 == 0;
     return a;
 }
 
@@ -434,6 +440,15 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     // (four times the workgroups); the partial sums stay in a.kpart until the
     // next layer's ln_shift (or, after the last layer, add_parts) adds them to h.
     const bool ffn_split = Tc == 1 && e.decode_fusion && !e.w_h && M <= 64 && d <= 1024 && hid % (16 * kFfnParts) == 0;
+    // Decode activations that only feed the decode GEMMs (the token-shift mixes,
+    // the WKV output and gate, the FFN hidden rows) are written in 16 x 16 tiles
+    // (tile_index), so those GEMMs read their A rows as contiguous 1 KB runs.
+    // Needs the fused step (low-rank stage and FFN split), one round of k steps
+    // per wave (d <= 768) and room for whole 16-row tiles.
+    // With several stream groups (parallel graph branches) a group's tiles must
+    // not cover another group's rows: whole tiles only.
+    const bool tl = ffn_split && e.act_tiles && a.tile_aligned && (e.branches == 1 || M % 16 == 0) && d % 16 == 0 &&
+                    d <= 768 && wkv7_step_lowrank_ok(s.head_size, L) && ((M + 15) / 16) * 16 <= e.max_tokens;
     for (int l = 0; l < s.layers; ++l) {
         const LayerW &w = e.layers[l];
         float *prev = e.st_prev + (size_t)l * e.max_streams * d;
@@ -444,7 +459,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
             // The previous layer's FFN output may be pending as K-split partials.
             const int np = ffn_split && l > 0 ? kFfnParts : 0;
             ENG_TRY(launch_ln_shift(a.h, n, d, w.ln_t_w, w.ln_t_b, prev, a.slots, w.mix6, a.mix, plane,
-                                    np ? a.kpart : nullptr, a.kplane, np, st), "ln_shift");
+                                    np ? a.kpart : nullptr, a.kplane, np, tl, st), "ln_shift");
         } else if (d <= 1024) {
             // LayerNorm + token shift in one pass; the last normed row of each
             // stream goes through a.hl (free until the LM head) to prev.
@@ -472,6 +487,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
                                 make_gemm(e, M, L, d, ma, d, w.a1t, d, la, L),
                                 make_gemm(e, M, L, d, mg, d, w.g1t, d, lg, L)};
             if (M <= 64) {
+                for (GemmParams &gp : g6) gp.a_tiled = tl;
                 if ((rc = gemm_group(st, g6, 6)) != YUF_OK) return rc;
             } else {
                 if ((rc = gemm_group(st, g6, 3)) != YUF_OK) return rc;
@@ -493,10 +509,11 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
             // The step kernel computes w, alpha and g from the rank-L rows.
             wp.lr = a.lr; wp.lr_plane = lplane; wp.L = L;
             wp.w2t = w.w2t; wp.a2t = w.a2t; wp.g2t = w.g2t; wp.w0 = w.w0; wp.a0 = w.a0; wp.g_out = a.g;
+            wp.tiled_out = tl;
         }
         ENG_TRY(launch_wkv7(wp, s.head_size, true, st), "wkv7");
-        if ((rc = ln_gemm(e, st, M, d, d, a.y, d, w.ln_o_w, w.ln_o_b, a.g, a.z, w.w_o, a.h, d, nullptr, a.h, d)) !=
-            YUF_OK)
+        if ((rc = ln_gemm(e, st, M, d, d, a.y, d, w.ln_o_w, w.ln_o_b, a.g, a.z, w.w_o, a.h, d, nullptr, a.h, d, false,
+                          tl)) != YUF_OK)
             return rc;
         // ROSA
         if ((rc = ln_gemm(e, st, M, 3 * D, d, a.h, d, w.ln_r_w, w.ln_r_b, nullptr, a.xn, w.rosa_w3, a.rosa3, 3 * D,
@@ -536,14 +553,18 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         }
         // FFN
         if ((rc = ln_gemm(e, st, M, 2 * hid, d, a.h, d, w.ln_f_w, w.ln_f_b, nullptr, a.xn, w.ffn_cat, a.ffn, hid,
-                          nullptr, nullptr, 0, true)) != YUF_OK)
+                          nullptr, nullptr, 0, true, false, tl)) != YUF_OK)
             return rc;
         if (ffn_split) {
             const int kp = hid / kFfnParts;
             GemmParams parts[kFfnParts];
-            for (int q = 0; q < kFfnParts; ++q)
-                parts[q] = make_gemm(e, M, d, kp, a.ffn + (size_t)q * kp, hid, w.ffn_out + (size_t)q * kp, hid,
+            for (int q = 0; q < kFfnParts; ++q) {
+                // Column q kp of the hidden rows: tile column q kp / 16 when tiled.
+                const float *aq = a.ffn + (tl ? tile_index(0, q * kp, hid) : (size_t)q * kp);
+                parts[q] = make_gemm(e, M, d, kp, aq, hid, w.ffn_out + (size_t)q * kp, hid,
                                      a.kpart + (size_t)q * a.kplane, d);
+                parts[q].a_tiled = tl;
+            }
             if ((rc = gemm_group(st, parts, kFfnParts)) != YUF_OK) return rc;
         } else if ((rc = gemm(e, st, M, d, hid, a.ffn, hid, w.ffn_out, hid, a.h, d, nullptr, ACT_NONE, a.h, d)) !=
                    YUF_OK) {
@@ -766,6 +787,7 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     e.s = s;
     if (const char *ng = std::getenv("YUF_NO_GRAPH")) e.use_graphs = std::strcmp(ng, "1") != 0;
     if (const char *rs = std::getenv("YUF_ROSA_SEGMENTED")) e.rosa_segmented = std::strcmp(rs, "0") != 0;
+    if (const char *dt = std::getenv("YUF_DECODE_TILES")) e.act_tiles = std::strcmp(dt, "0") != 0;
     if (const char *df = std::getenv("YUF_DECODE_FUSION")) e.decode_fusion = std::strcmp(df, "0") != 0;
     e.max_streams = max_streams;
     e.max_tokens = max_tokens;

@@ -734,7 +734,8 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
     const int g4 = lane >> 4, li = lane & 15;
     const int spw = ((p.K + KS - 1) / KS + kDecWaves - 1) / kDecWaves;  // k steps per wave
     const int k_begin = min(p.K, wave * spw * KS), k_end = min(p.K, k_begin + spw * KS);
-    const auto ra = make_rsrc(p.A + (size_t)row0 * p.lda, (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
+    const auto ra = make_rsrc(p.A + (size_t)row0 * p.lda, p.a_tiled ? (uint32_t)((size_t)RT * p.lda * 4)
+                                                                     : (uint32_t)(((size_t)(rows - 1) * p.lda + p.K) * 4));
     // Tiled W when given (contiguous 1 KB per wave load), else row-major W.
     const bool tiled = WB ? p.Wht != nullptr : p.Wt != nullptr;
     const uint32_t tiles_bytes = (uint32_t)((size_t)((p.N + 15) / 16) * p.wt_ld * (WB ? 2 : 4));
@@ -753,7 +754,9 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
     const auto rt = make_rsrc(PRO == 2 ? p.a_gate + (size_t)row0 * p.ldg : nullptr,
-                              PRO == 2 ? (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4) : 0u);
+                              PRO == 2 ? (p.a_tiled ? (uint32_t)((size_t)RT * p.ldg * 4)
+                                                    : (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4))
+                                       : 0u);
     auto load_w = [&](int s, int k0) {
         const int k = k0 + KS * s + RL * g4;
         const bool kin = k < k_end;  // K % RL == 0 on this path
@@ -772,13 +775,17 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
         for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int hh = 0; hh < AH; ++hh)
-                a[s][i][hh] = load4(ra, kin ? (uint32_t)((size_t)(16 * i + li) * p.lda + k + 4 * hh) * 4u : kBufferOob);
+                a[s][i][hh] = load4(ra, kin ? (uint32_t)(p.a_tiled ? tile_index(16 * i + li, k + 4 * hh, p.lda)
+                                                                   : (size_t)(16 * i + li) * p.lda + k + 4 * hh) * 4u
+                                            : kBufferOob);
         if constexpr (PRO == 2) {
 #pragma unroll
             for (int i = 0; i < MI; ++i)
 #pragma unroll
                 for (int hh = 0; hh < AH; ++hh)
-                    gt[s][i][hh] = load4(rt, kin ? (uint32_t)((size_t)(16 * i + li) * p.ldg + k + 4 * hh) * 4u : kBufferOob);
+                    gt[s][i][hh] = load4(rt, kin ? (uint32_t)(p.a_tiled ? tile_index(16 * i + li, k + 4 * hh, p.ldg)
+                                                                        : (size_t)(16 * i + li) * p.ldg + k + 4 * hh) * 4u
+                                                 : kBufferOob);
         }
     };
     // Issue order: with a prologue, all A (and gate) loads of the round first,
@@ -979,7 +986,7 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
         }
         if constexpr (NT == 2) {
             const int hcol = (w_row0 / 64) * 32 + (w_row0 % 64) + c;
-            p.C[(size_t)row * p.ldc + hcol] = x[0] / (1.0f + expf(-x[0])) * x[NT - 1];
+            p.C[p.c_tiled ? tile_index(row, hcol, p.ldc) : (size_t)row * p.ldc + hcol] = x[0] / (1.0f + expf(-x[0])) * x[NT - 1];
         } else {
             const int col = w_row0 + c;
             if (col < p.N) {
@@ -1539,6 +1546,10 @@ hipError_t launch_decode(const GemmParams *ps, int count, hipStream_t stream) {
     const int cap = dec_cap(NT, MI, PRO, WB);
     const int S = pick_steps(spw, cap);
     if (PRO == 2 && NT == 2) return hipErrorInvalidValue;
+    // A tiled A is read in the MFMA layout only: one round of k steps per wave
+    // (no later rounds and no row re-reads for the LayerNorm statistics).
+    for (int i = 0; i < count; ++i)
+        if ((ps[i].a_tiled || ps[i].c_tiled) && spw > S) return hipErrorInvalidValue;
     if (WB) launch_dec_kind<true>(g, NT, MI, PRO, S, grid, stream);
     else launch_dec_kind<false>(g, NT, MI, PRO, S, grid, stream);
     return hipGetLastError();
@@ -1617,6 +1628,7 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
     // Buffer descriptors address at most 2^31 bytes per 128-row panel.
     if ((size_t)kBM * p.lda * 4 >= (1u << 31) || (size_t)kBN * p.ldw * 4 >= (1u << 31)) return hipErrorInvalidValue;
     if (!prologue_ok(p)) return hipErrorInvalidValue;
+    if ((p.a_tiled || p.c_tiled) && (!decode_ok(p) || wide_steps(p))) return hipErrorInvalidValue;  // decode kernel only
     if (const int ws = wide_steps(p)) return launch_wide(p, ws, stream);
     if (decode_ok(p)) return launch_decode(&p, 1, stream);
     if (p.Wh) return launch_gemm_group(&p, 1, stream);  // bf16 W: large-tile path or an error
@@ -1640,8 +1652,10 @@ hipError_t launch_gemm(const GemmParams &p, hipStream_t stream) {
 
 hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream) {
     if (count < 1 || count > kMaxGroup) return hipErrorInvalidValue;
-    for (int i = 0; i < count; ++i)
+    for (int i = 0; i < count; ++i) {
         if (ps[i].M > 0 && ps[i].N > 0 && !prologue_ok(ps[i])) return hipErrorInvalidValue;
+        if ((ps[i].a_tiled || ps[i].c_tiled) && !decode_ok(ps[i])) return hipErrorInvalidValue;  // decode kernel only
+    }
     {
         // Decode-shaped products: one launch per (SiLU flag, prologue kind, W type).
         GemmParams dec[12][kMaxGroup];

@@ -33,6 +33,9 @@ struct WkvParams {
     int L = 0;
     const float *w2t = nullptr, *a2t = nullptr, *g2t = nullptr, *w0 = nullptr, *a0 = nullptr;
     float *g_out = nullptr;
+    // T = 1 step only: y and g_out written in 16 x 16 tiles (tile_index with
+    // row = sequence, column = h * N + channel, ld = H * N) for the decode GEMM.
+    bool tiled_out = false;
 };
 bool wkv7_supported(int N);
 // The fused low-rank step exists for N <= 64 and L <= 128 with L % 8 == 0.
@@ -115,6 +118,10 @@ struct GemmParams {
     const float *Wt = nullptr;
     const uint16_t *Wht = nullptr;
     int wt_ld = 0;
+    // Decode kernels only: A (and a_gate) stored in 16 x 16 tiles (tile_index,
+    // row strides lda / ldg), and, for the SiLU-pair product, C written that way
+    // (row stride ldc).  A tiled A needs one round of k steps per wave.
+    bool a_tiled = false, c_tiled = false;
 };
 hipError_t launch_gemm(const GemmParams &p, hipStream_t stream);
 
@@ -172,7 +179,7 @@ hipError_t launch_token_shift(const float *x, int Bn, int T, int d, const float 
 // floats apart, rows of width d) first, and the completed row is written back.
 hipError_t launch_ln_shift(float *x, int n, int d, const float *gamma, const float *beta, float *prev_state,
                            const int *slot, const float *mix6, float *out6, size_t out_stride, const float *parts,
-                           size_t part_stride, int nparts, hipStream_t stream);
+                           size_t part_stride, int nparts, bool out_tiled, hipStream_t stream);
 // x[m] += parts[0][m] + parts[1][m] + ... in order (M rows of width d).
 hipError_t launch_add_parts(float *x, int M, int d, const float *parts, size_t part_stride, int nparts,
                             hipStream_t stream);

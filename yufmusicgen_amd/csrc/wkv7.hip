@@ -437,7 +437,9 @@ __global__ void __launch_bounds__(kStepThreads * SPW) wkv7_step_kernel(WkvParams
             if constexpr (PAIR) dot += dpp_move<dpp::kQuadXor1>(dot);
             if (hj == 0) {
                 if (m == 2) {
-                    if (live) p.g_out[(size_t)bb * p.H * N + h * N + c] = 1.0f / (1.0f + expf(-dot));
+                    if (live)
+                        p.g_out[p.tiled_out ? tile_index(bb, h * N + c, p.H * N) : (size_t)bb * p.H * N + h * N + c] =
+                            1.0f / (1.0f + expf(-dot));
                 } else {
                     lrv[sub][m][c] = dot;
                 }
@@ -520,7 +522,7 @@ __global__ void __launch_bounds__(kStepThreads * SPW) wkv7_step_kernel(WkvParams
         float yv = 0.0f;
 #pragma unroll
         for (int u = 0; u < RQ; ++u) yv += part[sub][tid * RQ + u];
-        p.y[base + tid] = yv;
+        p.y[p.tiled_out ? tile_index(bb, h * N + tid, p.H * N) : base + tid] = yv;
     }
 }
 
@@ -575,8 +577,10 @@ hipError_t launch_wkv7(const WkvParams &p, int N, bool prep, hipStream_t stream)
     const char *force = std::getenv("YUF_WKV7_KERNEL");
     const bool want_serial = force && std::strcmp(force, "serial") == 0;
     const bool want_chunked = force && std::strcmp(force, "chunked") == 0;
-    // The fused low-rank form is the single-token step kernel only.
+    // The fused low-rank form is the single-token step kernel only, and so are
+    // tiled outputs (which the fused form's callers use).
     if (p.lr && (p.T != 1 || !prep)) return hipErrorInvalidValue;
+    if (p.tiled_out && !p.lr) return hipErrorInvalidValue;
     if (!p.lr && wkv7_chunk_supported(N) && !want_serial && (want_chunked || p.T >= kWkvChunkMinT))
         return launch_wkv7_chunked(p, N, prep, stream);
     switch (N) {
