@@ -534,3 +534,29 @@ def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n
         eng.close()
     np.testing.assert_allclose(out["1"][0], out["0"][0], rtol=0, atol=1e-4)
     np.testing.assert_allclose(out["1"][1], out["0"][1], rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("n", [40, 64])
+def test_tiled_decode_activations_are_bit_identical(tmp_path, monkeypatch, n):
+    """The 16 x 16-tiled decode activations (token-shift mixes, WKV output and
+    gate, FFN hidden rows) change only where values live, not the arithmetic:
+    logits and every carried state equal the row-major path's
+    (YUF_DECODE_TILES=0) bit for bit, including a ragged last 16-row tile (n = 40)."""
+    cfg = PRESETS["0.1b"]
+    weights = synth_weights(cfg, seed=17)
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, weights)
+    ck = Checkpoint.load(path)
+    slots = np.random.default_rng(8).permutation(n + 5)[:n].astype(np.int32)
+    prompt = uniform_tokens(21, n, 5, cfg.vocab_size)
+    steps = uniform_tokens(22, n, 3, cfg.vocab_size)
+    out = {}
+    for tiles in ("1", "0"):
+        monkeypatch.setenv("YUF_DECODE_TILES", tiles)
+        eng = Engine(ck, max_streams=n + 5, max_tokens=n * 5)
+        eng.prefill(prompt, slots=slots, logits="none")
+        logits = [eng.step(steps[:, t], slots=slots) for t in range(steps.shape[1])]
+        out[tiles] = (np.stack(logits), _states_from_blob(eng, slots))
+        eng.close()
+    np.testing.assert_array_equal(out["1"][0], out["0"][0])
+    np.testing.assert_array_equal(out["1"][1], out["0"][1])
