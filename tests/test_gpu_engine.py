@@ -158,6 +158,38 @@ def test_tiny_model_prompt_and_greedy_match_reference(golden_dir, tmp_path):
         np.testing.assert_allclose(last, z["greedy_logits"][i], rtol=0, atol=LOGIT_ATOL)
 
 
+def test_c1_tiny_greedy_256_steps_vs_oracle(tmp_path):
+    """C1 as configured: the tiny model (2 layers,
+    d = 128, 4 x 32 heads, ROSA 32, V = 512), a 32-token prompt, then 256
+    greedy decode steps, each fed the float64 oracle's own greedy choice: the
+    engine's logits within 1e-3 of the oracle's at every step and its argmax
+    equal to the oracle's wherever the top-2 gap exceeds 1e-3; final states
+    within 1e-4."""
+    cfg = PRESETS["tiny"]
+    weights = synth_weights(cfg, seed=41)
+    path = tmp_path / "c1.yuf"
+    write_yuf(path, cfg, weights)
+    prompt = prompt_tokens(42, 1, 32, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=1, max_tokens=64)
+    got = eng.prefill(prompt, logits="last")[0]
+    oracle = OracleModel(cfg.to_dict(), weights)
+    ref, state = oracle.forward(prompt)
+    ref = ref.numpy()[0, -1]
+    sure_steps = 0
+    for t in range(256):
+        np.testing.assert_allclose(got, ref, rtol=0, atol=LOGIT_ATOL, err_msg=f"step {t}")
+        top2 = np.sort(ref)[-2:]
+        if top2[1] - top2[0] > LOGIT_ATOL:
+            assert int(np.argmax(got)) == int(np.argmax(ref)), f"step {t}"
+            sure_steps += 1
+        tok = int(np.argmax(ref))
+        got = eng.step([tok])[0]
+        out, state = oracle.step(np.array([tok]), state)
+        ref = out.numpy()[0]
+    assert sure_steps > 200
+    np.testing.assert_allclose(_states_from_blob(eng, [0]), state_to_blob(state), rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.parametrize("steps", [80, 160, 256])
 def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path, steps):
     """The 0.1B architecture (14L, d=640, 16x40, ROSA 128, V=20480) on a short
