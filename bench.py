@@ -152,7 +152,7 @@ def bench_rosa(iters: int) -> dict:
     achieved = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "kernel": "rosa operator, segmented (rosa_power/scan/carry/final; C3 layer: B=8 T=2048 D=128)",
+            "kernel": "rosa operator, segmented (rosa_power/scan/carry/scan; C3 layer: B=8 T=2048 D=128)",
             "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
 
 

@@ -100,7 +100,7 @@ int yuf_rosa_scan_f32(int B, int T, int D,
  * allocate device memory (code under HIP graph capture, serving loops and
  * harnesses that forbid hipMalloc).  Same arguments, semantics and results.
  * The segmented form (T % 64 == 0, T >= 128, D in {64, 128, 256}) keeps its
- * scratch -- D * D + 3 * B * (T / 64) * D floats -- in a static 16 MiB device
+ * scratch -- D * D + 2 * B * (T / 64) * D floats -- in a static 16 MiB device
  * array (4,194,304 floats) that every GPU the library runs on holds until the
  * process ends; larger calls fail with YUF_ERR_INVALID.  Other shapes use no
  * scratch.  All calls on one GPU share that array: calls that overlap on one

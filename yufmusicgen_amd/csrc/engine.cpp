@@ -87,7 +87,7 @@ struct Engine {
     float *h = nullptr, *xn = nullptr, *mix = nullptr, *r = nullptr, *k = nullptr, *v = nullptr, *wr = nullptr,
           *al = nullptr, *g = nullptr, *lr = nullptr, *y = nullptr, *z = nullptr, *rosa3 = nullptr, *rread = nullptr,
           *ffn = nullptr, *hl = nullptr;
-    float *rz = nullptr, *rcarry = nullptr, *rends = nullptr;  // segmented ROSA scratch
+    float *rz = nullptr, *rcarry = nullptr;  // segmented ROSA scratch
     float *kpart = nullptr;  // [kFfnParts][max_streams][d]: K-split partials of the decode FFN output
     bool rosa_segmented = true;                                // YUF_ROSA_SEGMENTED=0 disables
     bool decode_fusion = true;                                 // YUF_DECODE_FUSION=0: separate low-rank GEMM and ROSA step
@@ -383,7 +383,7 @@ int gemm_group(hipStream_t st, const GemmParams *ps, int count) {
 struct Act {
     hipStream_t st = nullptr;
     float *h, *xn, *mix, *r, *k, *v, *wr, *al, *g, *lr, *y, *z, *rosa3, *rread, *ffn, *hl;
-    float *rz, *rcarry, *rends;  // segmented ROSA scratch (segment rows of kRosaSeg tokens)
+    float *rz, *rcarry;  // segmented ROSA scratch (segment rows of kRosaSeg tokens)
     const int *tokens, *slots;
     int *bad;     // out-of-range token flag the embedding sets
     int *rcount;  // fused ROSA-out tile counters of this group of streams
@@ -405,7 +405,7 @@ Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
     a.ffn = e.ffn + m0 * 4 * d;
     a.hl = e.hl + (size_t)s0 * d;
     const size_t seg0 = (m0 / kRosaSeg) * s.rosa;
-    a.rz = e.rz + seg0; a.rcarry = e.rcarry + seg0; a.rends = e.rends + seg0;
+    a.rz = e.rz + seg0; a.rcarry = e.rcarry + seg0;
     a.tokens = e.tokens_dev + m0;
     a.slots = e.slots_dev + s0;
     a.bad = e.bad_dev;
@@ -544,7 +544,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
             rp.decay = w.rosa_decay; rp.direction = w.rosa_hh; rp.raw_params = true;
             rp.memory_in = ros; rp.memory_out = ros; rp.slot = a.slots; rp.read_out = a.rread;
             if (e.rosa_segmented && Tc > 1 && rosa_segmented_ok(Tc, D, kRosaSeg)) {
-                ENG_TRY(launch_rosa_segmented(rp, w.rosa_al, kRosaSeg, a.rz, a.rcarry, a.rends, st), "rosa segmented");
+                ENG_TRY(launch_rosa_segmented(rp, w.rosa_al, kRosaSeg, a.rz, a.rcarry, st), "rosa segmented");
             } else {
                 ENG_TRY(launch_rosa(rp, st), "rosa");
             }
@@ -926,14 +926,14 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     const size_t sizes[] = {Mx * d, Mx * d, 6 * Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d, Mx * d,
                             3 * Mx * s.low_rank, Mx * d, Mx * d, Mx * 3 * s.rosa, Mx * s.rosa, Mx * 4 * d,
                             (size_t)max_streams * d, ws, Mx / kRosaSeg * s.rosa + s.rosa, Mx / kRosaSeg * s.rosa + s.rosa,
-                            Mx / kRosaSeg * s.rosa + s.rosa, (size_t)kFfnParts * max_streams * d};
+                            (size_t)kFfnParts * max_streams * d};
     size_t total = 0;
     for (size_t z : sizes) total += ((z * sizeof(float) + 255) / 256) * 256;
     ENG_TRY(hipMalloc(&e.work.p, total), "workspace alloc");
     {
         char *cur = static_cast<char *>(e.work.p);
         float **dst[] = {&e.h, &e.xn, &e.mix, &e.r, &e.k, &e.v, &e.wr, &e.al, &e.g, &e.lr, &e.y, &e.z, &e.rosa3,
-                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.rends, &e.kpart};
+                         &e.rread, &e.ffn, &e.hl, &e.gemm_ws, &e.rz, &e.rcarry, &e.kpart};
         for (size_t i = 0; i < sizeof(sizes) / sizeof(sizes[0]); ++i) *dst[i] = carve<float>(cur, sizes[i]);
     }
     const size_t io_bytes = 256 * 5 + (size_t)(2 * max_streams + max_tokens + 2) * sizeof(int);

@@ -64,17 +64,22 @@ struct RosaParams {
     // gate sigmoid(read_raw), same indexing as the pre-activations; when set,
     // cand / write / read_raw are ignored and the read is gated.
     const float *e_pre = nullptr, *g_pre = nullptr;
+    // Segmented second pass: the B rows are chains of `seg` consecutive
+    // segments, and only each chain's last segment writes its end state, to
+    // memory_out row seg_slot[chain] (or chain).
+    int seg = 0;
+    const int *seg_slot = nullptr;
 };
 hipError_t launch_rosa(const RosaParams &p, hipStream_t stream);
 // Long sequences with the model's constant transition A = diag(lambda) H: the
 // T tokens of each chain split into T / L segments scanned in parallel (zero
 // start, then true start) around a carry pass with AL = A^L ([D][D] row-major,
-// fp32).  Scratch: z, carry, ends of B * (T / L) * D floats each.
+// fp32).  Scratch: z, carry of B * (T / L) * D floats each.
 bool rosa_segmented_ok(int T, int D, int L);
 // A^L of A = diag(lambda) (I - 2 u u^T) into AL [D][D] (column j = A^L e_j),
 // computed in double on the device (lambda post-sigmoid, u unit).
 hipError_t launch_rosa_power(int D, int L, const float *lambda, const float *u, float *AL, hipStream_t stream);
-hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry, float *ends,
+hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry,
                                  hipStream_t stream);
 
 // ----------------------------------------------------------------------- GEMM

@@ -320,11 +320,19 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
         }
         lds_barrier();
     }
-    if (wave == 0 && p.memory_out) {
+    // End state: every row, or (segmented second pass) each chain's last segment.
+    int out_row = slot;
+    bool write_out = p.memory_out != nullptr;
+    if (p.seg > 0) {
+        const int chain = bb / p.seg;
+        write_out = write_out && bb - chain * p.seg == p.seg - 1;
+        out_row = p.seg_slot ? p.seg_slot[chain] : chain;
+    }
+    if (wave == 0 && write_out) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const int c = lane + e * kWave;
-            if (c < D) p.memory_out[(size_t)slot * D + c] = m0[e];
+            if (c < D) p.memory_out[(size_t)out_row * D + c] = m0[e];
         }
     }
 }
@@ -436,13 +444,6 @@ __global__ void __launch_bounds__(1024) rosa_carry_kernel(int P, int D, const fl
     }
 }
 
-__global__ void rosa_final_kernel(int P, int D, const float *ends, const int *slot, float *memory_out) {
-    const int b = blockIdx.x;
-    const int sl = slot ? slot[b] : b;
-    for (int c = threadIdx.x; c < D; c += blockDim.x)
-        memory_out[(size_t)sl * D + c] = ends[((size_t)b * P + P - 1) * D + c];
-}
-
 // A^L of the ROSA transition A = diag(lambda) (I - 2 u u^T) for the operator
 // path (lambda post-sigmoid, u unit), in double precision like the engine's
 // host-side copy: wave w of workgroup g applies A L times to e_j, j = 4 g + w,
@@ -493,7 +494,7 @@ bool rosa_segmented_ok(int T, int D, int L) {
     return L > 0 && T % L == 0 && T / L >= 2 && (D == 64 || D == 128 || D == 256);
 }
 
-hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry, float *ends,
+hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, float *z, float *carry,
                                  hipStream_t stream) {
     if (p.B <= 0) return hipSuccess;
     if (!rosa_segmented_ok(p.T, p.D, L)) return hipErrorInvalidValue;
@@ -508,15 +509,13 @@ hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, fl
     hipLaunchKernelGGL(rosa_carry_kernel, dim3(p.B), dim3(p.D * p.D / 64), 0, stream, P, p.D, AL, z, p.memory_in,
                        p.slot, carry);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    // 3. every segment again from its true start: the reads and end states.
+    // 3. every segment again from its true start: the reads, and the last
+    // segment's end state as the chain's new state.
     RosaParams c = p;
     c.B = p.B * P; c.T = L;
-    c.memory_in = carry; c.slot = nullptr; c.memory_out = ends;
-    if ((e = launch_rosa(c, stream)) != hipSuccess) return e;
-    // 4. the last segment's end state is the chain's new state.
-    if (p.memory_out)
-        hipLaunchKernelGGL(rosa_final_kernel, dim3(p.B), dim3(256), 0, stream, P, p.D, ends, p.slot, p.memory_out);
-    return hipGetLastError();
+    c.memory_in = carry; c.slot = nullptr;
+    c.seg = P; c.seg_slot = p.slot;
+    return launch_rosa(c, stream);
 }
 
 namespace {
@@ -584,7 +583,7 @@ namespace yuf {
 namespace {
 
 // The no-allocation operator variant (yuf_rosa_scan_f32_noalloc) keeps the
-// segmented scan's scratch -- A^L and the z / carry / ends segment rows -- in
+// segmented scan's scratch -- A^L and the z / carry segment rows -- in
 // this file-scope device array: every device the library runs on holds one
 // copy, at its own address, until the process ends.  Nothing in it needs to
 // start at zero (each pass writes its rows before the next reads them).
@@ -637,11 +636,11 @@ int rosa_operator(int B, int T, int D, const float *cand, const float *write, co
         // segments from zero, the carry chain, and segments from their starts.
         float *buf = nullptr;
         const size_t seg = (size_t)B * (T / kOpRosaSeg) * D;
-        const size_t need = (size_t)D * D + 3 * seg;
+        const size_t need = (size_t)D * D + 2 * seg;
         if (noalloc) {
             if (need > kNoAllocScratchFloats)
                 return fail(YUF_ERR_INVALID, "rosa noalloc: B * (T / 64) * D = " + std::to_string(seg) +
-                                                 " needs " + std::to_string(need) + " scratch floats (D^2 + 3 B (T / 64) D); "
+                                                 " needs " + std::to_string(need) + " scratch floats (D^2 + 2 B (T / 64) D); "
                                                  "the static buffer holds " + std::to_string(kNoAllocScratchFloats) +
                                                  " -- split the batch or use yuf_rosa_scan_f32");
             int rc = noalloc_scratch(&buf);
@@ -649,9 +648,9 @@ int rosa_operator(int B, int T, int D, const float *cand, const float *write, co
         } else if ((err = op_rosa_scratch(st, need, &buf)) != hipSuccess) {
             return fail(YUF_ERR_OOM, std::string("rosa scratch: ") + hipGetErrorString(err));
         }
-        float *AL = buf, *z = AL + (size_t)D * D, *carry = z + seg, *ends = carry + seg;
+        float *AL = buf, *z = AL + (size_t)D * D, *carry = z + seg;
         err = launch_rosa_power(D, kOpRosaSeg, decay, direction, AL, st);
-        if (err == hipSuccess) err = launch_rosa_segmented(p, AL, kOpRosaSeg, z, carry, ends, st);
+        if (err == hipSuccess) err = launch_rosa_segmented(p, AL, kOpRosaSeg, z, carry, st);
     } else {
         err = launch_rosa(p, st);
     }
