@@ -47,6 +47,24 @@ def test_wkv7_matches_oracle(size, steps, wkv_kernel):
     np.testing.assert_allclose(s.cpu().numpy(), se.numpy(), rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("wkv_kernel", ["chunked"], indirect=True)
+@pytest.mark.parametrize("size", [8, 40])
+def test_wkv7_many_heads_one_workgroup_each(size, wkv_kernel):
+    """More than 128 heads (here 9 x 16 = 144) run one workgroup per head
+    instead of two; with N = 40 (and N = 8) the last 16-key tile is half
+    padding and takes the permuted half-tile form."""
+    from yufmusicgen_amd.ops import rwkv7_scan
+
+    print(f"wkv7 unsplit N={size}", flush=True)
+    arrs = wkv_inputs(300 + size, 9, 37, 16, size)
+    s0 = np.random.default_rng(size + 1).standard_normal((9, 16, size, size)).astype(np.float32) * 0.3
+    y, s = rwkv7_scan(*(_dev(x) for x in arrs), state=_dev(s0))
+    ye, se = _oracle_wkv(arrs, s0)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(y.cpu().numpy(), ye.numpy(), rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(s.cpu().numpy(), se.numpy(), rtol=RTOL, atol=ATOL)
+
+
 def test_wkv7_reference_golden(golden_dir):
     from yufmusicgen_amd.ops import rwkv7_scan
 

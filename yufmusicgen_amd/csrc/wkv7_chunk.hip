@@ -72,6 +72,9 @@ __device__ __forceinline__ floatx4 mfma(float a, float b, floatx4 c) {
 
 __device__ __forceinline__ floatx4 ld4(const float *p) { return *reinterpret_cast<const floatx4 *>(p); }
 
+typedef float floatx2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ floatx2 ld2(const float *p) { return *reinterpret_cast<const floatx2 *>(p); }
+
 __device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t rsrc, uint32_t byte_offset) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, byte_offset, 0, 0));
 }
@@ -149,7 +152,13 @@ template <int NB> struct RoleMap<NB, true> : SplitRoles<NB> {
 
 // SPLIT: two workgroups per head; the first owns value tiles [0, (NB + 1) / 2),
 // the second the rest.
-template <int NB, bool PREP, bool SPLIT>
+// HALF (N % 16 == 8): the last key tile holds 8 keys.  Its accumulator row
+// m = 4 g + r stands for key 16 (NB - 1) + 8 (r >> 1) + 2 g + (r & 1), so the
+// real keys sit in registers r = 0, 1 of every lane group, and every product
+// over the keys takes k-steps r = 0, 1 only on that tile (k-step r of lane
+// group g: key 2 g + r of the tile) instead of four k-steps of which half
+// would multiply zeros.
+template <int NB, bool PREP, bool SPLIT, bool HALF>
 __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
     wkv7_chunk_kernel(WkvParams p, int N, int units, int per_xcd) {
     using Ly = Lds<NB, SPLIT>;
@@ -176,6 +185,29 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
     if (role < NB && role >= nv) role = kRoleIdle;
     const int g = lane >> 4, li = lane & 15;
     const int T = p.T, HN = p.H * N;
+    constexpr int kLast = NB - 1;
+    auto half_tile = [](int jb) { return HALF && jb == kLast; };
+    auto ksteps = [&](int jb) { return half_tile(jb) ? 2 : 4; };
+    // Key of accumulator row m of tile jb.
+    auto rowkey = [&](int jb, int m) {
+        return 16 * jb + (half_tile(jb) ? ((m & 2) << 2) + 2 * (m >> 2) + (m & 1) : m);
+    };
+    // The k-step values of lane group g over tile jb of a [token][key] row.
+    auto ldk = [&](const float *row, int jb) -> floatx4 {
+        if (half_tile(jb)) {
+            const floatx2 v = ld2(row + 16 * jb + 2 * g);
+            return floatx4{v[0], v[1], 0.0f, 0.0f};
+        }
+        return ld4(row + 16 * jb + 4 * g);
+    };
+    // g_15 of the four accumulator rows of lane group g in tile jb.
+    auto ldg = [&](const float *gl, int jb) -> floatx4 {
+        if (half_tile(jb)) {
+            const floatx2 a = ld2(gl + 16 * jb + 2 * g), b = ld2(gl + 16 * jb + 8 + 2 * g);
+            return floatx4{a[0], a[1], b[0], b[1]};
+        }
+        return ld4(gl + 16 * jb + 4 * g);
+    };
     const int n_chunks = (T + kC - 1) / kC;
     // Per-(b, h) token-major views: element (t, c) at t * HN + c.  Tokens past
     // T fall outside the descriptor range and read as 0.
@@ -206,10 +238,11 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                     floatx4 Y0 = {0.f, 0.f, 0.f, 0.f}, Y1 = Y0;
 #pragma unroll
                     for (int jb = 0; jb < NB; ++jb) {
-                        const floatx4 r4 = ld4(sA + Ly::oRs + li * SA + 16 * jb + 4 * g);
+                        const floatx4 r4 = ldk(sA + Ly::oRs + li * SA, jb);
                         const floatx4 s0 = xt[jb * 64 + lane];
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
+                            if (r >= ksteps(jb)) break;
                             if (r & 1) Y1 = mfma(r4[r], s0[r], Y1);
                             else Y0 = mfma(r4[r], s0[r], Y0);
                         }
@@ -240,6 +273,12 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                                       p.state_in ? (uint32_t)(N * N * 4) : 0u);
 #pragma unroll
             for (int jb = 0; jb < NB; ++jb) {
+                if (half_tile(jb)) {
+                    const int j0 = 16 * jb + 2 * g;  // rows r = 0, 1; rows 2, 3 are padding keys
+                    S[jb] = floatx4{buf_load(rs, i < N ? (uint32_t)(i * N + j0) * 4u : kBufferOob),
+                                    buf_load(rs, i < N ? (uint32_t)(i * N + j0 + 1) * 4u : kBufferOob), 0.0f, 0.0f};
+                    continue;
+                }
                 const int j0 = 16 * jb + 4 * g;
                 S[jb] = buf_load4(rs, (i < N && j0 < N) ? (uint32_t)(i * N + j0) * 4u : kBufferOob);
             }
@@ -259,10 +298,11 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                 floatx4 X0 = {0.f, 0.f, 0.f, 0.f}, X1 = X0;
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
-                    const floatx4 a4 = ld4(sA + Ly::oAs + li * SA + 16 * jb + 4 * g);
+                    const floatx4 a4 = ldk(sA + Ly::oAs + li * SA, jb);
                     xt[jb * 64 + lane] = S[jb];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (r >= ksteps(jb)) break;
                         if (r & 1) X1 = mfma(a4[r], S[jb][r], X1);
                         else X0 = mfma(a4[r], S[jb][r], X0);
                     }
@@ -281,9 +321,10 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                 xt[NB * 64 + lane] = U;
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
-                    const floatx4 gl4 = ld4(sA + Ly::oGl + 16 * jb + 4 * g);
-                    const floatx4 bh4 = ld4(sA + Ly::oBhT + (16 * jb + li) * kST + 4 * g);
-                    const floatx4 kh4 = ld4(sA + Ly::oKhT + (16 * jb + li) * kST + 4 * g);
+                    const floatx4 gl4 = ldg(sA + Ly::oGl, jb);
+                    const int brow = rowkey(jb, li);
+                    const floatx4 bh4 = ld4(sA + Ly::oBhT + brow * kST + 4 * g);
+                    const floatx4 kh4 = ld4(sA + Ly::oKhT + brow * kST + 4 * g);
                     floatx4 acc = S[jb];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc = mfma(bh4[r], U[r], acc);
@@ -300,10 +341,11 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                 floatx4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
-                    const floatx4 a4 = ld4(sA + Ly::oAs + li * SA + 16 * jb + 4 * g);
-                    const floatx4 r4 = ld4(sA + Ly::oRs + li * SA + 16 * jb + 4 * g);
+                    const floatx4 a4 = ldk(sA + Ly::oAs + li * SA, jb);
+                    const floatx4 r4 = ldk(sA + Ly::oRs + li * SA, jb);
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (r >= ksteps(jb)) break;
                         X = mfma(a4[r], S[jb][r], X);
                         Y = mfma(r4[r], S[jb][r], Y);
                     }
@@ -325,9 +367,10 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                 // S^T <- diag(g_15) (S^T + B^^T U + K^^T V)
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
-                    const floatx4 gl4 = ld4(sA + Ly::oGl + 16 * jb + 4 * g);
-                    const floatx4 bh4 = ld4(sA + Ly::oBhT + (16 * jb + li) * kST + 4 * g);
-                    const floatx4 kh4 = ld4(sA + Ly::oKhT + (16 * jb + li) * kST + 4 * g);
+                    const floatx4 gl4 = ldg(sA + Ly::oGl, jb);
+                    const int brow = rowkey(jb, li);
+                    const floatx4 bh4 = ld4(sA + Ly::oBhT + brow * kST + 4 * g);
+                    const floatx4 kh4 = ld4(sA + Ly::oKhT + brow * kST + 4 * g);
                     floatx4 acc = S[jb];
 #pragma unroll
                     for (int r = 0; r < 4; ++r) acc = mfma(bh4[r], U[r], acc);
@@ -347,6 +390,12 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
             const auto rs = make_rsrc(p.state_out + state_off, (uint32_t)(N * N * 4));
 #pragma unroll
             for (int jb = 0; jb < NB; ++jb) {
+                if (half_tile(jb)) {
+                    const int j0 = 16 * jb + 2 * g;
+                    buf_store(S[jb][0], rs, i < N ? (uint32_t)(i * N + j0) * 4u : kBufferOob);
+                    buf_store(S[jb][1], rs, i < N ? (uint32_t)(i * N + j0 + 1) * 4u : kBufferOob);
+                    continue;
+                }
                 const int j0 = 16 * jb + 4 * g;
                 buf_store4(S[jb], rs, (i < N && j0 < N) ? (uint32_t)(i * N + j0) * 4u : kBufferOob);
             }
@@ -501,18 +550,19 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
                 floatx4 gab = {0.f, 0.f, 0.f, 0.f}, gp = gab, gqb = gab, gqk = gab;
 #pragma unroll
                 for (int jb = 0; jb < NB; ++jb) {
-                    const int o = li * SA + 16 * jb + 4 * g;
-                    const floatx4 a4 = ld4(sA + Ly::oAs + o), r4 = ld4(sA + Ly::oRs + o);
-                    // B^[s = li][key 16 jb + 4 g + r] from the [key][token] tiles.
-                    const int oT = (16 * jb + 4 * g) * kST + li;
-                    floatx4 b4, k4;
+                    const floatx4 a4 = ldk(sA + Ly::oAs + li * SA, jb), r4 = ldk(sA + Ly::oRs + li * SA, jb);
+                    // B^[s = li][key of k-step r] from the [key][token] tiles.
+                    const int oT = (16 * jb + (half_tile(jb) ? 2 : 4) * g) * kST + li;
+                    floatx4 b4 = {0.f, 0.f, 0.f, 0.f}, k4 = b4;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (r >= ksteps(jb)) break;
                         b4[r] = sA[Ly::oBhT + oT + r * kST];
                         k4[r] = sA[Ly::oKhT + oT + r * kST];
                     }
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
+                        if (r >= ksteps(jb)) break;
                         gab = mfma(a4[r], b4[r], gab);
                         gp = mfma(a4[r], k4[r], gp);
                         gqb = mfma(r4[r], b4[r], gqb);
@@ -628,15 +678,28 @@ __global__ void __launch_bounds__((RoleMap<NB, SPLIT>::kWaves) * kWave)
 // MI355X has 256 CUs; one workgroup per head would leave half of them idle).
 constexpr int kSplitMaxHeads = 128;
 
+template <int NB, bool SPLIT, bool HALF>
+void launch_nb_form(const WkvParams &p, int N, bool prep, int units, int per_xcd, hipStream_t stream) {
+    const dim3 grid(per_xcd * kXcds), block(RoleMap<NB, SPLIT>::kWaves * kWave);
+    if (prep)
+        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, true, SPLIT, HALF>), grid, block, 0, stream, p, N, units, per_xcd);
+    else
+        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, false, SPLIT, HALF>), grid, block, 0, stream, p, N, units, per_xcd);
+}
+
+// Half-padded last key tile (N % 16 == 8) unless YUF_WKV7_HALF=0.
+bool half_tile_form(int N) {
+    if (N % 16 != 8) return false;
+    const char *e = std::getenv("YUF_WKV7_HALF");
+    return !(e && std::strcmp(e, "0") == 0);
+}
+
 template <int NB, bool SPLIT>
 hipError_t launch_nb_split(const WkvParams &p, int N, bool prep, hipStream_t stream) {
     const int heads = p.B * p.H, units = SPLIT ? 2 * heads : heads;
     const int per_xcd = (units + kXcds - 1) / kXcds;
-    const dim3 grid(per_xcd * kXcds), block(RoleMap<NB, SPLIT>::kWaves * kWave);
-    if (prep)
-        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, true, SPLIT>), grid, block, 0, stream, p, N, units, per_xcd);
-    else
-        hipLaunchKernelGGL((wkv7_chunk_kernel<NB, false, SPLIT>), grid, block, 0, stream, p, N, units, per_xcd);
+    if (half_tile_form(N)) launch_nb_form<NB, SPLIT, true>(p, N, prep, units, per_xcd, stream);
+    else launch_nb_form<NB, SPLIT, false>(p, N, prep, units, per_xcd, stream);
     return hipGetLastError();
 }
 
