@@ -99,7 +99,7 @@ def bench_scan(iters: int) -> dict:
             traffic = json.load(handle).get("traffic_bytes")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "wkv7_chunk_kernel<3,false,true> (C2: B=8 T=2048 H=16 N=40; two workgroups per head)",
+            "kernel": "wkv7_chunk_kernel<3,false,true,true> (C2: B=8 T=2048 H=16 N=40; two workgroups per head, half-padded last key tile)",
             "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
 
 
