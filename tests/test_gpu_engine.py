@@ -216,6 +216,40 @@ def test_default_model_short_prefill_and_decode_vs_oracle(tmp_path, steps):
     np.testing.assert_allclose(blob, state_to_blob(state), rtol=1e-4, atol=1e-4)
 
 
+def test_c3_full_size_prefill_vs_oracle(tmp_path):
+    """C3 at its configured size: the 0.1B model prefills B = 8 x T = 2048 in one
+    pass (every prefill kernel at its benchmark shape: 256-row GEMM tiles of
+    M = 16,384, the split WKV-7 scan over 128 heads, 32 segmented ROSA
+    segments per sequence).  Sequences 0 and 5 against the float64 oracle at
+    full length (last-position logits within 1e-3, carried states within
+    1e-4); all eight against the same prefill run as two T-chunks of 1024
+    that carry the state (logits within 1e-4, states within 1e-4)."""
+    cfg = PRESETS["0.1b"]
+    weights = synth_weights(cfg, seed=51)
+    path = tmp_path / "c3.yuf"
+    write_yuf(path, cfg, weights)
+    ck = Checkpoint.load(path)
+    tokens = uniform_tokens(52, 8, 2048, cfg.vocab_size)
+    eng = Engine(ck, max_streams=8, max_tokens=8 * 2048)
+    last = eng.prefill(tokens, logits="last")
+    states = _states_from_blob(eng, range(8))
+    eng.close()
+    oracle = OracleModel(cfg.to_dict(), weights)
+    for b in (0, 5):
+        print(f"C3 full size: oracle sequence {b}", flush=True)
+        ref, st = oracle.forward(tokens[b:b + 1])
+        np.testing.assert_allclose(last[b], ref.numpy()[0, -1], rtol=0, atol=LOGIT_ATOL, err_msg=f"sequence {b}")
+        np.testing.assert_allclose(states[b], state_to_blob(st)[0], rtol=1e-4, atol=1e-4, err_msg=f"sequence {b}")
+        del ref
+    chunked = Engine(ck, max_streams=8, max_tokens=8 * 1024)
+    last2 = chunked.prefill(tokens, logits="last")
+    states2 = _states_from_blob(chunked, range(8))
+    print(f"C3 two T-chunks vs one pass: logits {np.abs(last2 - last).max():.2e}, "
+          f"states {np.abs(states2 - states).max():.2e}", flush=True)
+    np.testing.assert_allclose(last2, last, rtol=0, atol=1e-4)
+    np.testing.assert_allclose(states2, states, rtol=1e-4, atol=1e-4)
+
+
 def test_wide_model_prefill_and_decode_vs_oracle(tmp_path):
     """The C5 architecture (24L, d=1024, 16x64 heads, ROSA 256, V=20480) in fp32
     on 2 x 128 tokens plus decode steps, against the float64 oracle: the N = 64
