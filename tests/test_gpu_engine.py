@@ -439,6 +439,41 @@ def test_c4_shape_64_streams_32_steps_vs_oracle(tmp_path):
     np.testing.assert_allclose(blob, state_to_blob(state), rtol=1e-4, atol=1e-4)
 
 
+def test_c4_as_configured_1024_steps_vs_oracle(tmp_path):
+    """C4 as configured: 64 streams of the 0.1B
+    model, each prefilled with 256 tokens, then 1024 decode steps replayed
+    from the step graph.  The engine runs all 64 streams; the float64 oracle
+    follows four of them (teacher-forced with the same tokens): their logits
+    within 1e-3 at every step, greedy ids identical wherever the oracle's
+    top-2 gap exceeds 1e-3, and their carried states within 1e-4 after the
+    last step."""
+    cfg = PRESETS["0.1b"]
+    weights = synth_weights(cfg, seed=61)
+    path = tmp_path / "c4.yuf"
+    write_yuf(path, cfg, weights)
+    n, prompt_len, steps = 64, 256, 1024
+    follow = [0, 21, 42, 63]
+    prompt = uniform_tokens(62, n, prompt_len, cfg.vocab_size)
+    nxt = uniform_tokens(63, n, steps, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=n, max_tokens=n * prompt_len)
+    got = eng.prefill(prompt, logits="last")
+    oracle = OracleModel(cfg.to_dict(), weights)
+    ref, state = oracle.forward(prompt[follow])
+    np.testing.assert_allclose(got[follow], ref.numpy()[:, -1], rtol=0, atol=LOGIT_ATOL)
+    worst = 0.0
+    for t in range(steps):
+        g = eng.step(nxt[:, t])[follow]
+        r, state = oracle.step(nxt[follow, t], state)
+        r = r.numpy()
+        worst = max(worst, float(np.abs(g - r).max()))
+        np.testing.assert_allclose(g, r, rtol=0, atol=LOGIT_ATOL, err_msg=f"step {t}")
+        top2 = np.sort(r, axis=1)[:, -2:]
+        sure = top2[:, 1] - top2[:, 0] > LOGIT_ATOL
+        assert np.array_equal(np.argmax(g, 1)[sure], np.argmax(r, 1)[sure]), f"step {t}"
+    print(f"C4: 64 streams x {steps} steps, 4 followed: worst logit deviation {worst:.2e}", flush=True)
+    np.testing.assert_allclose(_states_from_blob(eng, follow), state_to_blob(state), rtol=1e-4, atol=1e-4)
+
+
 def test_c5_bf16_24_layers_vs_fp32_oracle(tmp_path):
     """C5 as configured: 24 layers, d = 1024, 16 x 64
     heads, ROSA 256, V = 20480, bf16 projection weights (a version-2 .yuf) with
