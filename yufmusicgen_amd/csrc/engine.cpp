@@ -113,11 +113,13 @@ struct Engine {
     int step_n = 0;
     const int32_t *step_tok = nullptr;
     float *step_logits = nullptr;
-    // The step can split its streams into `branches` groups replayed on their
-    // own HIP streams (fork / join events): independent chains of small
-    // kernels that the hardware queues overlap.  YUF_DECODE_BRANCHES=1..4.
+    // The step can split its streams into groups replayed on their own HIP
+    // streams (fork / join events): independent chains of small kernels that
+    // the hardware queues overlap.  branches = 0: automatic (two groups when
+    // n is a multiple of 32 and at least 64, else one); YUF_DECODE_BRANCHES=1..4
+    // forces that many groups.
     static constexpr int kMaxBranches = 4;
-    int branches = 1;
+    int branches = 0;
     hipStream_t side[kMaxBranches - 1] = {};
     hipEvent_t fork = nullptr, join[kMaxBranches - 1] = {};
 
@@ -390,6 +392,7 @@ struct Act {
     float *kpart;  // FFN-out K-split partials of these streams, planes kplane floats apart
     size_t kplane;
     bool tile_aligned;  // the rows start at a multiple of 16 (16 x 16-tiled decode activations possible)
+    bool grouped = false;  // one of several stream groups of a step (parallel graph branches)
 };
 
 Act act_at(Engine &e, hipStream_t st, int s0, int Tc) {
@@ -447,7 +450,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     // per wave (d <= 768) and room for whole 16-row tiles.
     // With several stream groups (parallel graph branches) a group's tiles must
     // not cover another group's rows: whole tiles only.
-    const bool tl = ffn_split && e.act_tiles && a.tile_aligned && (e.branches == 1 || M % 16 == 0) && d % 16 == 0 &&
+    const bool tl = ffn_split && e.act_tiles && a.tile_aligned && (!a.grouped || M % 16 == 0) && d % 16 == 0 &&
                     d <= 768 && wkv7_step_lowrank_ok(s.head_size, L) && ((M + 15) / 16) * 16 <= e.max_tokens;
     for (int l = 0; l < s.layers; ++l) {
         const LayerW &w = e.layers[l];
@@ -681,7 +684,9 @@ int drop_step_graphs(Engine &e) {
 // and the LM head over all n streams (its weights are read once per step).
 int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
     if (!e.use_graphs) return prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
-    const int G = std::max(1, std::min(e.branches, n));
+    // Measured on MI355X (0.1B model, 64 streams): one group 0.975 ms per step,
+    // two 0.953, three 1.068 (21-row groups: no whole tiles), four 1.030.
+    const int G = e.branches > 0 ? std::max(1, std::min(e.branches, n)) : (n >= 64 && n % 32 == 0 ? 2 : 1);
     auto group = [&](int g) { return std::make_pair((int)((long long)n * g / G), (int)((long long)n * (g + 1) / G)); };
     auto stream_of = [&](int g) { return g == 0 ? e.stream : e.side[g - 1]; };
     if (!(e.step_exec[0] && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
@@ -702,6 +707,7 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
                 hipStream_t st = stream_of(g);
                 rc = capture(st, [&]() {
                     Act a = act_at(e, st, s0, 1);
+                    a.grouped = true;
                     a.tokens = tokens_dev + s0;
                     a.bad = flag_for(e, tokens_dev);
                     return forward_pass(e, a, s1 - s0, 1, nullptr, YUF_LOGITS_NONE, 1, 0);
@@ -802,12 +808,10 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
         return fail(YUF_ERR_OOM, "out of host memory preparing weights");
     }
     ENG_TRY(hipStreamCreateWithFlags(&e.stream, hipStreamNonBlocking), "stream create");
-    // Measured on MI355X (0.1B, 64 streams): 1 branch 1.49 ms per step, 2: 1.55,
-    // 3: 1.66, 4: 2.12 -- the groups' kernels contend more than they overlap.
-    e.branches = 1;
-    if (const char *b = std::getenv("YUF_DECODE_BRANCHES")) e.branches = std::atoi(b);
-    e.branches = std::max(1, std::min(e.branches, (int)Engine::kMaxBranches));
-    for (int i = 0; i + 1 < e.branches; ++i) {
+    e.branches = 0;  // automatic
+    if (const char *b = std::getenv("YUF_DECODE_BRANCHES"))
+        e.branches = std::max(1, std::min(std::atoi(b), (int)Engine::kMaxBranches));
+    for (int i = 0; i + 1 < std::max(e.branches, 2); ++i) {
         ENG_TRY(hipStreamCreateWithFlags(&e.side[i], hipStreamNonBlocking), "side stream create");
         ENG_TRY(hipEventCreateWithFlags(&e.join[i], hipEventDisableTiming), "event create");
     }
