@@ -751,14 +751,17 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
         for (int i = 0; i < MI; ++i) acc[t][i] = floatx4{0.f, 0.f, 0.f, 0.f};
     floatx4 a[S][MI][AH], b[S][NT];  // b: 4 fp32 W values, or 8 bf16 ones (raw bits)
     floatx4 gt[PRO == 2 ? S : 1][MI][AH];
-    auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    // The loaders are forced inline: left as calls (the inliner's choice at
+    // S = 10 and at MI = 4), a and b are passed by address and live in scratch
+    // memory, which made those instantiations about 13x slower.
+    auto load4 =[](__amdgpu_buffer_rsrc_t rs, uint32_t off) __attribute__((always_inline)) {
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
     const auto rt = make_rsrc(PRO == 2 ? p.a_gate + (size_t)row0 * p.ldg : nullptr,
                               PRO == 2 ? (p.a_tiled ? (uint32_t)((size_t)RT * p.ldg * 4)
                                                     : (uint32_t)(((size_t)(rows - 1) * p.ldg + p.K) * 4))
                                        : 0u);
-    auto load_w = [&](int s, int k0) {
+    auto load_w = [&](int s, int k0) __attribute__((always_inline)) {
         const int k = k0 + KS * s + RL * g4;
         const bool kin = k < k_end;  // K % RL == 0 on this path
 #pragma unroll
@@ -769,7 +772,7 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
             b[s][t] = load4(rw, (kin && wr < p.N) ? (uint32_t)e * (WB ? 2u : 4u) : kBufferOob);
         }
     };
-    auto load_a = [&](int s, int k0) {
+    auto load_a = [&](int s, int k0) __attribute__((always_inline)) {
         const int k = k0 + KS * s + RL * g4;
         const bool kin = k < k_end;
 #pragma unroll
@@ -791,7 +794,7 @@ __global__ void __launch_bounds__(kDecThreads) gemm_decode_kernel(DecodeGroup g)
     };
     // Issue order: with a prologue, all A (and gate) loads of the round first,
     // so the row statistics wait for A only while W is still in flight.
-    auto load_round = [&](int k0) {
+    auto load_round = [&](int k0) __attribute__((always_inline)) {
         if constexpr (PRO > 0) {
 #pragma unroll
             for (int s = 0; s < S; ++s) load_a(s, k0);
@@ -1020,7 +1023,7 @@ __global__ void __launch_bounds__(kDecThreads) gemm_wide_kernel(GemmParams p, in
     const bool tiled = p.Wt != nullptr;  // 16 x 16 tiles: one contiguous 1 KB run per wave load
     const auto rw = tiled ? make_rsrc(p.Wt, (uint32_t)((size_t)((p.N + 15) / 16) * p.wt_ld * 4))
                           : make_rsrc(p.W, (uint32_t)(((size_t)(p.N - 1) * p.ldw + K) * 4));
-    auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    auto load4 = [](__amdgpu_buffer_rsrc_t rs, uint32_t off) __attribute__((always_inline)) {
         return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     };
     floatx4 a[S][4];
@@ -1032,7 +1035,7 @@ __global__ void __launch_bounds__(kDecThreads) gemm_wide_kernel(GemmParams p, in
             a[s][i] = load4(ra, row < M && k < K ? (uint32_t)((size_t)row * p.lda + k) * 4u : kBufferOob);
         }
     floatx4 b0[S], b1[S];
-    auto load_w = [&](floatx4 (&b)[S], int slice) {
+    auto load_w = [&](floatx4 (&b)[S], int slice) __attribute__((always_inline)) {
         const int wr = slice * 16 + li;
 #pragma unroll
         for (int s = 0; s < S; ++s) {

@@ -65,7 +65,11 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <int EPL>
+// EMIT = false: end states only (the first pass of the segmented scan), so
+// neither the reads nor their gate are computed and the gate input is not
+// loaded.  A compile-time switch: as a run-time flag its tests inside the
+// unrolled load loops made the scan ~35 % slower at D = 256.
+template <int EPL, bool EMIT>
 __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
     using K = Cfg<EPL>;
     constexpr int C = K::C, DP = K::DP, ZS = K::ZS, CH = K::CH, CPL = K::CPL;
@@ -92,28 +96,26 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
     const int pw = wave < 4 ? wave - 1 : wave - 2;  // producer index on waves 1-3, 5-7
     const bool producer = wave != 0 && wave != 4;
     const bool prepared = p.e_pre != nullptr;
-    // Without reads to emit (the first pass of the segmented scan: end states
-    // only) the read gate is never used, so its input is not loaded.
-    const bool want_gate = gated && p.read_out != nullptr;
     // Next chunk's inputs, loaded one iteration ahead: (cand, write, read_raw) or,
-    // prepared, (e, gate).
-    float in0[K::kItems], in1[K::kItems] = {}, in2[K::kItems] = {};
+    // prepared, (e, gate).  Every load is issued; an input that is not needed
+    // has a zero-size descriptor and reads 0 without touching memory.
+    float in0[K::kItems], in1[K::kItems], in2[K::kItems];
     auto load_in = [&](int ch) {
         const int t0 = ch * C, nt = min(C, p.T - t0);
         const size_t base = (size_t)(bb * p.T + t0) * p.ld;
         const uint32_t bytes = (uint32_t)(((nt - 1) * p.ld + D) * 4);
         const auto r0 = make_rsrc((prepared ? p.e_pre : p.cand) + base, bytes);
-        const auto r1 = make_rsrc((prepared ? p.g_pre : p.write) + base, prepared && !want_gate ? 0u : bytes);
-        const auto r2 = make_rsrc(want_gate && !prepared ? p.read_raw + base : p.cand + base,
-                                  want_gate && !prepared ? bytes : 0u);
+        const auto r1 = make_rsrc((prepared ? p.g_pre : p.write) + base, EMIT || !prepared ? bytes : 0u);
+        const auto r2 = make_rsrc(gated && !prepared ? p.read_raw + base : p.cand + base,
+                                  gated && !prepared ? bytes : 0u);
 #pragma unroll
         for (int it = 0; it < K::kItems; ++it) {
             const int q = lane + it * kWave;
             const int tau = q / CH, c = pw * CH + (q - tau * CH);
             const uint32_t off = (q < C * CH && c < D && tau < nt) ? (uint32_t)(tau * p.ld + c) * 4u : kBufferOob;
             in0[it] = buf_load(r0, off);
-            if (!prepared || want_gate) in1[it] = buf_load(r1, off);
-            if (want_gate && !prepared) in2[it] = buf_load(r2, off);
+            in1[it] = buf_load(r1, off);
+            in2[it] = EMIT ? buf_load(r2, off) : 0.0f;
         }
     };
     auto stage_in = [&](int ch) {  // A(ch), from the registers load_in(ch) filled
@@ -126,13 +128,13 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
                 float e, gv;
                 if (prepared) {
                     e = in0[it];
-                    gv = want_gate ? in1[it] : 1.0f;
+                    gv = EMIT ? in1[it] : 1.0f;
                 } else {
                     // tanh(x) = 1 - 2 / (e^{2x} + 1); sigmoid(x) = 1 / (1 + e^{-x}).  Out-of-range
                     // tokens and channels read 0 and give e = 0.
                     const float th = 1.0f - 2.0f * __frcp_rn(__expf(2.0f * in0[it]) + 1.0f);
                     e = th * __frcp_rn(1.0f + __expf(-in1[it]));
-                    gv = want_gate ? __frcp_rn(1.0f + __expf(-in2[it])) : 1.0f;
+                    gv = EMIT && gated ? __frcp_rn(1.0f + __expf(-in2[it])) : 1.0f;
                 }
                 ew[s][tau * DP + c] = e;
                 gt[s][tau * DP + c] = gv;
@@ -156,7 +158,7 @@ __global__ void __launch_bounds__(kThreads) rosa_scan_kernel(RosaParams p) {
         }
     };
     auto emit = [&](int ch) {  // O(ch)
-        if (!p.read_out) return;  // end states only (first pass of the segmented scan)
+        if constexpr (!EMIT) return;
         const int s = ch % kStages, t0 = ch * C, nt = min(C, p.T - t0);
         const size_t obase = (size_t)(bb * p.T + t0) * D;
         const auto ro = make_rsrc(p.read_out + obase, (uint32_t)(nt * D * 4));
@@ -568,12 +570,21 @@ hipError_t launch_rosa(const RosaParams &p, hipStream_t stream) {
     }
     const dim3 grid(p.B), block(kThreads);
     const int epl = (p.D + kWave - 1) / kWave;
-    if (epl <= 1) hipLaunchKernelGGL(rosa_scan_kernel<1>, grid, block, 0, stream, p);
-    else if (epl <= 2) hipLaunchKernelGGL(rosa_scan_kernel<2>, grid, block, 0, stream, p);
-    else if (epl <= 4) hipLaunchKernelGGL(rosa_scan_kernel<4>, grid, block, 0, stream, p);
-    else if (epl <= 8) hipLaunchKernelGGL(rosa_scan_kernel<8>, grid, block, 0, stream, p);
-    else if (epl <= 16) hipLaunchKernelGGL(rosa_scan_kernel<16>, grid, block, 0, stream, p);
-    else return hipErrorInvalidValue;
+    if (p.read_out) {
+        if (epl <= 1) hipLaunchKernelGGL((rosa_scan_kernel<1, true>), grid, block, 0, stream, p);
+        else if (epl <= 2) hipLaunchKernelGGL((rosa_scan_kernel<2, true>), grid, block, 0, stream, p);
+        else if (epl <= 4) hipLaunchKernelGGL((rosa_scan_kernel<4, true>), grid, block, 0, stream, p);
+        else if (epl <= 8) hipLaunchKernelGGL((rosa_scan_kernel<8, true>), grid, block, 0, stream, p);
+        else if (epl <= 16) hipLaunchKernelGGL((rosa_scan_kernel<16, true>), grid, block, 0, stream, p);
+        else return hipErrorInvalidValue;
+    } else {
+        if (epl <= 1) hipLaunchKernelGGL((rosa_scan_kernel<1, false>), grid, block, 0, stream, p);
+        else if (epl <= 2) hipLaunchKernelGGL((rosa_scan_kernel<2, false>), grid, block, 0, stream, p);
+        else if (epl <= 4) hipLaunchKernelGGL((rosa_scan_kernel<4, false>), grid, block, 0, stream, p);
+        else if (epl <= 8) hipLaunchKernelGGL((rosa_scan_kernel<8, false>), grid, block, 0, stream, p);
+        else if (epl <= 16) hipLaunchKernelGGL((rosa_scan_kernel<16, false>), grid, block, 0, stream, p);
+        else return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -404,18 +404,20 @@ __global__ void __launch_bounds__(NTH) sample_kernel(SampleParams p) {
         if (best < k) {
             token = cand_idx[best];
         } else {
-            // Position best >= k of the host's order: the (best - k)-th
-            // smallest id outside the candidates (all -inf, in id order).
-            int ids[kMaxTopK];
-            for (int i = 0; i < k; ++i) ids[i] = cand_idx[i];
-            for (int i = 1; i < k; ++i)
-                for (int j = i; j > 0 && ids[j - 1] > ids[j]; --j) {
-                    const int t = ids[j];
-                    ids[j] = ids[j - 1];
-                    ids[j - 1] = t;
-                }
-            int x = best - k;
-            for (int i = 0; i < k; ++i) x += ids[i] <= x ? 1 : 0;
+            // Position best >= k of the host's order: the t-th (t = best - k,
+            // from 0) smallest id outside the candidates (all -inf, in id
+            // order).  That id is the least x >= t with x = t + #{candidate
+            // ids <= x}; iterating x <- t + count(x) from x = t climbs to it
+            // (count is non-decreasing) in at most k + 1 rounds, with no
+            // sorted copy of the ids (a private array would live in scratch).
+            const int t = best - k;
+            int x = t;
+            for (int round = 0; round <= k; ++round) {
+                int c = 0;
+                for (int i = 0; i < k; ++i) c += cand_idx[i] <= x ? 1 : 0;
+                if (t + c == x) break;
+                x = t + c;
+            }
             token = x;
         }
         p.tokens[s] = token < V ? token : 0;
