@@ -22,7 +22,8 @@ from yufmusicgen_amd import build as yuf_build
 # Kernel-name pattern -> largest allowed scratch (bytes per lane) and why.
 ALLOWED_SCRATCH = {
     # The unsplit N = 64 chunk scan with fused prep (the C5 shape): its
-    # 12-wave workgroup leaves 168 VGPRs per lane, and the compiler spills 4.
+    # 10-wave workgroup (three waves on some SIMDs) leaves 168 VGPRs per lane,
+    # and the compiler spills 4.
     r"wkv7_chunk_kernelILi4ELb1ELb0ELb[01]E": 20,
 }
 
