@@ -380,6 +380,30 @@ def test_rosa_segmented_prefill_matches_sequential(tmp_path, monkeypatch):
         np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("max_tokens,logits", [(4 * 256, "all"), (4 * 128, "all"), (4 * 256, "last")])
+def test_prefill_stream_groups_are_bit_identical(tmp_path, monkeypatch, max_tokens, logits):
+    """A prefill whose parts (>= 256 rows each) run on two or four HIP streams
+    against the whole batch on one stream (YUF_PREFILL_GROUPS=1): logits and
+    states bit for bit, in one pass, in carried T-chunks, and with
+    last-position logits; scattered slots so each part indexes the state
+    through its own slots."""
+    cfg = PRESETS["0.1b"]
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=12))
+    ck = Checkpoint.load(path)
+    tokens = uniform_tokens(13, 4, 256, cfg.vocab_size)
+    slots = [5, 0, 3, 6]
+    outs = []
+    for groups in ("1", "2", "4"):
+        monkeypatch.setenv("YUF_PREFILL_GROUPS", groups)
+        eng = Engine(ck, max_streams=7, max_tokens=max_tokens)
+        got = eng.prefill(tokens, slots=slots, logits=logits)
+        outs.append((got, _states_from_blob(eng, slots)))
+    for other in outs[1:]:
+        for a, b in zip(outs[0], other):
+            np.testing.assert_array_equal(a, b)
+
+
 def test_wide_decode_batch_vs_oracle(tmp_path):
     """40 streams of the 0.1B architecture: the decode products take 16-row
     tiles with a ragged last tile (16 + 16 + 8), the LayerNorm prologues, the

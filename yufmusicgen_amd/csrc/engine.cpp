@@ -92,6 +92,7 @@ struct Engine {
     bool rosa_segmented = true;                                // YUF_ROSA_SEGMENTED=0 disables
     bool decode_fusion = true;                                 // YUF_DECODE_FUSION=0: separate low-rank GEMM and ROSA step
     bool act_tiles = true;                                     // YUF_DECODE_TILES=0: row-major decode activations
+    int prefill_groups = 0;                                    // YUF_PREFILL_GROUPS=1..4: streams for the batch's parts (0: automatic)
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
     size_t gemm_ws_floats = 0;
     // Out-of-range token flags set by the embedding kernel: bad_host for the
@@ -635,10 +636,32 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         }
         const bool last_chunk = t0 + tc >= T;
         const int chunk_mode = mode == YUF_LOGITS_ALL ? YUF_LOGITS_ALL : (last_chunk ? mode : YUF_LOGITS_NONE);
-        Act a = act_at(e, e.stream, 0, tc);
-        a.bad = flag_for(e, tokens_dev);
-        int rc = forward_pass(e, a, n, tc, logits_dev, chunk_mode, T, t0);
-        if (rc != YUF_OK) return rc;
+        // Parts of the batch on their own HIP streams when each part has at
+        // least 256 rows: one part's latency-bound kernels (the scans, the
+        // LayerNorms) run beside another part's GEMMs.  The parts touch
+        // disjoint workspace rows, state slots and logit rows.  Automatic
+        // count, measured on MI355X: four parts when the batch has at most 128
+        // heads (C3, 8 x 2048: 25.5 ms per step as one part, 25.2 as two, 24.3
+        // as three, 24.0 as four), else two (C5, 32 x 2048 chunks: bf16
+        // prefill 722 ms as one part, 672 as two, 698 as four).
+        int G = e.prefill_groups > 0 ? e.prefill_groups : ((size_t)n * e.s.heads <= 128 ? 4 : 2);
+        G = std::min(G, n);
+        while (G > 1 && (size_t)(n / G) * tc < 256) --G;
+        if (G > 1) ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
+        for (int g = G - 1; g >= 0; --g) {
+            const int s0 = (int)((long long)n * g / G), s1 = (int)((long long)n * (g + 1) / G);
+            hipStream_t st = g == 0 ? e.stream : e.side[g - 1];
+            if (g > 0) ENG_TRY(hipStreamWaitEvent(st, e.fork, 0), "fork wait");
+            Act a = act_at(e, st, s0, tc);
+            a.bad = flag_for(e, tokens_dev);
+            float *lg = logits_dev;
+            if (lg && chunk_mode == YUF_LOGITS_ALL) lg += (size_t)s0 * T * e.s.vocab;
+            else if (lg && chunk_mode == YUF_LOGITS_LAST) lg += (size_t)s0 * e.s.vocab;
+            const int rc = forward_pass(e, a, s1 - s0, tc, lg, chunk_mode, T, t0);
+            if (rc != YUF_OK) return rc;
+            if (g > 0) ENG_TRY(hipEventRecord(e.join[g - 1], st), "join record");
+        }
+        for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
     }
     return YUF_OK;
 }
@@ -794,6 +817,7 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     if (const char *ng = std::getenv("YUF_NO_GRAPH")) e.use_graphs = std::strcmp(ng, "1") != 0;
     if (const char *rs = std::getenv("YUF_ROSA_SEGMENTED")) e.rosa_segmented = std::strcmp(rs, "0") != 0;
     if (const char *dt = std::getenv("YUF_DECODE_TILES")) e.act_tiles = std::strcmp(dt, "0") != 0;
+    if (const char *pg = std::getenv("YUF_PREFILL_GROUPS")) e.prefill_groups = std::max(1, std::min(std::atoi(pg), Engine::kMaxBranches));
     if (const char *df = std::getenv("YUF_DECODE_FUSION")) e.decode_fusion = std::strcmp(df, "0") != 0;
     e.max_streams = max_streams;
     e.max_tokens = max_tokens;
@@ -811,7 +835,7 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     e.branches = 0;  // automatic
     if (const char *b = std::getenv("YUF_DECODE_BRANCHES"))
         e.branches = std::max(1, std::min(std::atoi(b), (int)Engine::kMaxBranches));
-    for (int i = 0; i + 1 < std::max(e.branches, 2); ++i) {
+    for (int i = 0; i + 1 < Engine::kMaxBranches; ++i) {
         ENG_TRY(hipStreamCreateWithFlags(&e.side[i], hipStreamNonBlocking), "side stream create");
         ENG_TRY(hipEventCreateWithFlags(&e.join[i], hipEventDisableTiming), "event create");
     }
