@@ -352,7 +352,8 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards data-parallel over streams, see DESIGN.md)", file=sys.stderr)
+              "(the path would shard data-parallel over streams: one engine per GPU, each "
+              "holding its own streams' recurrent state)", file=sys.stderr)
         return 2
 
     import torch
