@@ -380,23 +380,30 @@ def test_rosa_segmented_prefill_matches_sequential(tmp_path, monkeypatch):
         np.testing.assert_allclose(a, b, rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("max_tokens,logits", [(4 * 256, "all"), (4 * 128, "all"), (4 * 256, "last")])
-def test_prefill_stream_groups_are_bit_identical(tmp_path, monkeypatch, max_tokens, logits):
+@pytest.mark.parametrize("preset,n,max_tokens,logits,weights", [
+    ("0.1b", 4, 4 * 256, "all", "f32"),
+    ("0.1b", 4, 4 * 128, "all", "f32"),   # carried T-chunks
+    ("0.1b", 4, 4 * 256, "last", "f32"),
+    ("0.1b", 5, 5 * 256, "all", "f32"),   # uneven parts (1, 1, 1, 2 sequences)
+    ("wide2", 4, 4 * 256, "all", "bf16"),  # the bf16-weight large-tile kernels
+])
+def test_prefill_stream_groups_are_bit_identical(tmp_path, monkeypatch, preset, n, max_tokens, logits, weights):
     """A prefill whose parts (>= 256 rows each) run on two or four HIP streams
     against the whole batch on one stream (YUF_PREFILL_GROUPS=1): logits and
-    states bit for bit, in one pass, in carried T-chunks, and with
-    last-position logits; scattered slots so each part indexes the state
-    through its own slots."""
-    cfg = PRESETS["0.1b"]
+    states bit for bit, in one pass, in carried T-chunks, with last-position
+    logits, with uneven parts and with bf16 weights; scattered slots so each
+    part indexes the state through its own slots."""
+    import dataclasses
+    cfg = dataclasses.replace(PRESETS["wide"], n_layers=2) if preset == "wide2" else PRESETS[preset]
     path = tmp_path / "m.yuf"
     write_yuf(path, cfg, synth_weights(cfg, seed=12))
     ck = Checkpoint.load(path)
-    tokens = uniform_tokens(13, 4, 256, cfg.vocab_size)
-    slots = [5, 0, 3, 6]
+    tokens = uniform_tokens(13, n, 256, cfg.vocab_size)
+    slots = [5, 0, 3, 6, 2][:n]
     outs = []
     for groups in ("1", "2", "4"):
         monkeypatch.setenv("YUF_PREFILL_GROUPS", groups)
-        eng = Engine(ck, max_streams=7, max_tokens=max_tokens)
+        eng = Engine(ck, max_streams=7, max_tokens=max_tokens, weight_dtype=weights)
         got = eng.prefill(tokens, slots=slots, logits=logits)
         outs.append((got, _states_from_blob(eng, slots)))
     for other in outs[1:]:
