@@ -487,8 +487,11 @@ def main() -> int:
         "config": {
             "workload": "C3 prefill: 0.1B model (14L, d640, 16x40 heads, ROSA 128, V 20480, seeded fp32 weights), "
                         "B=8 x T=2048 token ids, all-position logits",
+            "prefill_streams": os.environ.get("YUF_PREFILL_GROUPS", "4 (automatic: the batch's 128 heads as four "
+                                                                    "parts of two sequences)"),
             "decode_workload": f"C4: 64 streams prefilled with 256 tokens, {args.decode_steps} steps, "
                                "device top-k=32 T=1.0 sampling",
+            "decode_streams": os.environ.get("YUF_DECODE_BRANCHES", "2 (automatic: two 32-stream step graphs)"),
         },
         "decode_tokens_per_s": round(decode_tps, 1),
         "decode_ms_per_step": round(dec_elapsed * 1e3 / args.decode_steps, 3),
