@@ -433,13 +433,17 @@ int lm_head_last(Engine &e, const Act &a, int n, int Tc, float *logits) {
 
 // One forward pass over n streams x Tc tokens whose ids and slots are in
 // a.tokens / a.slots.  logits: LAST -> [n, V] at `logits`; ALL -> row (b, t) at
-// logits + (b * row_stride_T + t0 + t) * V.
-int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode, int row_stride_T, int t0) {
+// logits + (b * row_stride_T + t0 + t) * V.  [l_begin, l_end) limits the pass
+// to those layers: the embedding runs with l_begin = 0, the LM head with the
+// last layer (l_end = -1: through the last layer).
+int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode, int row_stride_T, int t0,
+                 int l_begin = 0, int l_end = -1) {
     const ModelShape &s = e.s;
     const int M = n * Tc, d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4 * s.d;
     const size_t plane = (size_t)e.max_tokens * d, lplane = (size_t)e.max_tokens * L;
     hipStream_t st = a.st;
-    ENG_TRY(launch_embed(a.tokens, M, e.emb, d, V, a.h, a.bad, st), "embed");
+    if (l_end < 0 || l_end > s.layers) l_end = s.layers;
+    if (l_begin == 0) ENG_TRY(launch_embed(a.tokens, M, e.emb, d, V, a.h, a.bad, st), "embed");
     // Decode: the FFN output product is split over K into kFfnParts products
     // (four times the workgroups); the partial sums stay in a.kpart until the
     // next layer's ln_shift (or, after the last layer, add_parts) adds them to h.
@@ -453,7 +457,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     // not cover another group's rows: whole tiles only.
     const bool tl = ffn_split && e.act_tiles && a.tile_aligned && (!a.grouped || M % 16 == 0) && d % 16 == 0 &&
                     d <= 768 && wkv7_step_lowrank_ok(s.head_size, L) && ((M + 15) / 16) * 16 <= e.max_tokens;
-    for (int l = 0; l < s.layers; ++l) {
+    for (int l = l_begin; l < l_end; ++l) {
         const LayerW &w = e.layers[l];
         float *prev = e.st_prev + (size_t)l * e.max_streams * d;
         float *wkv = e.st_wkv + (size_t)l * e.max_streams * e.wkv_floats();
@@ -575,6 +579,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
             return rc;
         }
     }
+    if (l_end < s.layers) return YUF_OK;  // more layers follow in another call
     if (ffn_split && s.layers > 0)
         ENG_TRY(launch_add_parts(a.h, M, d, a.kpart, a.kplane, kFfnParts, st), "ffn partials");
     if (mode == YUF_LOGITS_LAST) return lm_head_last(e, a, n, Tc, logits);
@@ -648,20 +653,36 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         G = std::min(G, n);
         while (G > 1 && (size_t)(n / G) * tc < 256) --G;
         if (G > 1) ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
-        for (int g = G - 1; g >= 0; --g) {
+        Act acts[Engine::kMaxBranches];
+        float *lgs[Engine::kMaxBranches];
+        int ns[Engine::kMaxBranches];
+        for (int g = 0; g < G; ++g) {
             const int s0 = (int)((long long)n * g / G), s1 = (int)((long long)n * (g + 1) / G);
             hipStream_t st = g == 0 ? e.stream : e.side[g - 1];
             if (g > 0) ENG_TRY(hipStreamWaitEvent(st, e.fork, 0), "fork wait");
-            Act a = act_at(e, st, s0, tc);
-            a.bad = flag_for(e, tokens_dev);
-            float *lg = logits_dev;
-            if (lg && chunk_mode == YUF_LOGITS_ALL) lg += (size_t)s0 * T * e.s.vocab;
-            else if (lg && chunk_mode == YUF_LOGITS_LAST) lg += (size_t)s0 * e.s.vocab;
-            const int rc = forward_pass(e, a, s1 - s0, tc, lg, chunk_mode, T, t0);
-            if (rc != YUF_OK) return rc;
-            if (g > 0) ENG_TRY(hipEventRecord(e.join[g - 1], st), "join record");
+            acts[g] = act_at(e, st, s0, tc);
+            acts[g].bad = flag_for(e, tokens_dev);
+            lgs[g] = logits_dev;
+            if (lgs[g] && chunk_mode == YUF_LOGITS_ALL) lgs[g] += (size_t)s0 * T * e.s.vocab;
+            else if (lgs[g] && chunk_mode == YUF_LOGITS_LAST) lgs[g] += (size_t)s0 * e.s.vocab;
+            ns[g] = s1 - s0;
         }
-        for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+        // Submitted a layer at a time across the parts, so every part starts
+        // at once instead of waiting for the host to enqueue the whole pass of
+        // the parts before it.
+        const int layers = e.s.layers;
+        for (int l = 0; l == 0 || l < layers; ++l) {
+            const int l1 = G > 1 ? std::min(l + 1, layers) : layers;
+            for (int g = 0; g < G; ++g) {
+                const int rc = forward_pass(e, acts[g], ns[g], tc, lgs[g], chunk_mode, T, t0, l, l1);
+                if (rc != YUF_OK) return rc;
+            }
+            if (l1 == layers) break;
+        }
+        for (int g = 1; g < G; ++g) {
+            ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
+            ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+        }
     }
     return YUF_OK;
 }
