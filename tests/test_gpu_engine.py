@@ -411,6 +411,38 @@ def test_prefill_stream_groups_are_bit_identical(tmp_path, monkeypatch, preset, 
             np.testing.assert_array_equal(a, b)
 
 
+def test_prefill_parts_and_decode_groups_interleaved(tmp_path, monkeypatch):
+    """Prefills in parts and graph-replayed decode steps in two stream groups
+    share the engine's side streams and fork / join events: alternate them
+    (64 streams, a second prefill of 32 of them into other slots, more steps)
+    and compare bit for bit with one part and one decode group."""
+    cfg = PRESETS["0.1b"]
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=14))
+    ck = Checkpoint.load(path)
+    first = uniform_tokens(15, 64, 128, cfg.vocab_size)
+    second = uniform_tokens(16, 32, 256, cfg.vocab_size)
+    steps = uniform_tokens(17, 64, 6, cfg.vocab_size)
+    slots_a = list(range(64))
+    slots_b = list(range(64, 96))
+    outs = []
+    for forced in (False, True):  # automatic (two parts, two groups), then one of each
+        for var in ("YUF_PREFILL_GROUPS", "YUF_DECODE_BRANCHES"):
+            if forced:
+                monkeypatch.setenv(var, "1")
+            else:
+                monkeypatch.delenv(var, raising=False)
+        eng = Engine(ck, max_streams=96, max_tokens=64 * 128)
+        got = [eng.prefill(first, slots=slots_a, logits="last")]
+        got += [eng.step(steps[:, t], slots=slots_a) for t in range(3)]
+        got.append(eng.prefill(second, slots=slots_b, logits="last"))
+        got += [eng.step(steps[:, t], slots=slots_a) for t in range(3, 6)]
+        got.append(_states_from_blob(eng, [0, 31, 63, 64, 95]))
+        outs.append(got)
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_wide_decode_batch_vs_oracle(tmp_path):
     """40 streams of the 0.1B architecture: the decode products take 16-row
     tiles with a ragged last tile (16 + 16 + 8), the LayerNorm prologues, the

@@ -431,6 +431,10 @@ int lm_head_last(Engine &e, const Act &a, int n, int Tc, float *logits) {
     return ln_gemm(e, a.st, n, V, d, last, d, e.ln_fin_w, e.ln_fin_b, nullptr, a.xn, e.head, logits, V);
 }
 
+// Internal logits mode of a prefill part: gather the last rows into a.hl for
+// one LM head over all parts after they join.
+constexpr int kLogitsGather = -1;
+
 // One forward pass over n streams x Tc tokens whose ids and slots are in
 // a.tokens / a.slots.  logits: LAST -> [n, V] at `logits`; ALL -> row (b, t) at
 // logits + (b * row_stride_T + t0 + t) * V.  [l_begin, l_end) limits the pass
@@ -583,6 +587,10 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     if (ffn_split && s.layers > 0)
         ENG_TRY(launch_add_parts(a.h, M, d, a.kpart, a.kplane, kFfnParts, st), "ffn partials");
     if (mode == YUF_LOGITS_LAST) return lm_head_last(e, a, n, Tc, logits);
+    if (mode == kLogitsGather) {  // a part of a prefill: its last rows only
+        if (Tc > 1) ENG_TRY(launch_gather_last(a.h, n, Tc, d, a.hl, st), "gather_last");
+        return YUF_OK;
+    }
     if (mode == YUF_LOGITS_ALL) {
         ENG_TRY(launch_layernorm(a.h, M, d, e.ln_fin_w, e.ln_fin_b, nullptr, a.xn, st), "ln_final");
         if (row_stride_T == Tc && t0 == 0) return gemm(e, st, M, V, d, a.xn, d, e.head, d, logits, V);
@@ -640,7 +648,7 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
                     "tokens copy");
         }
         const bool last_chunk = t0 + tc >= T;
-        const int chunk_mode = mode == YUF_LOGITS_ALL ? YUF_LOGITS_ALL : (last_chunk ? mode : YUF_LOGITS_NONE);
+        int chunk_mode = mode == YUF_LOGITS_ALL ? YUF_LOGITS_ALL : (last_chunk ? mode : YUF_LOGITS_NONE);
         // Parts of the batch on their own HIP streams when each part has at
         // least 256 rows: one part's latency-bound kernels (the scans, the
         // LayerNorms) run beside another part's GEMMs.  The parts touch
@@ -653,6 +661,11 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         G = std::min(G, n);
         while (G > 1 && (size_t)(n / G) * tc < 256) --G;
         if (G > 1) ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
+        // Last-position logits of a split batch: the parts gather their last
+        // rows and one LM head runs over all of them after the join (the same
+        // kernel, so the same values, as for the whole batch in one part).
+        const bool head_after = G > 1 && chunk_mode == YUF_LOGITS_LAST;
+        if (head_after) chunk_mode = kLogitsGather;
         Act acts[Engine::kMaxBranches];
         float *lgs[Engine::kMaxBranches];
         int ns[Engine::kMaxBranches];
@@ -682,6 +695,12 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         for (int g = 1; g < G; ++g) {
             ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
             ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+        }
+        if (head_after) {
+            const Act a0 = act_at(e, e.stream, 0, tc);
+            const int rc = ln_gemm(e, e.stream, n, e.s.vocab, e.s.d, tc > 1 ? e.hl : e.h, e.s.d, e.ln_fin_w,
+                                   e.ln_fin_b, nullptr, a0.xn, e.head, logits_dev, e.s.vocab);
+            if (rc != YUF_OK) return rc;
         }
     }
     return YUF_OK;
