@@ -106,7 +106,9 @@ int yuf_rosa_scan_f32(int B, int T, int D,
  * scratch.  All calls on one GPU share that array: calls that overlap on one
  * GPU (other streams, other host threads) race and must be ordered by the
  * caller.  The first call on a device resolves the array's address there
- * (hipGetSymbolAddress, not a stream operation).
+ * (hipGetSymbolAddress, not a stream operation).  YUF_ROSA_SEGMENTED does
+ * not apply to this entry point: shapes that admit the segmented form always
+ * take it, so the capacity check above runs before any launch.
  */
 int yuf_rosa_scan_f32_noalloc(int B, int T, int D,
                               const float *cand, const float *write, const float *read_raw,

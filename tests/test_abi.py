@@ -34,10 +34,13 @@ def test_errors_cross_the_abi_as_status_codes():
     assert rc == -1 and "D must be" in lib.yuf_last_error().decode()
 
 
-def test_noalloc_rosa_rejects_scratch_beyond_its_static_buffer():
+def test_noalloc_rosa_rejects_scratch_beyond_its_static_buffer(monkeypatch):
     """Checked on the host before any HIP call: B = 64, T = 8192, D = 256 needs
-    65536 + 3 * 64 * 128 * 256 floats, past the 4,194,304 of the buffer."""
+    D * D + 2 * B * (T / 64) * D = 65536 + 2 * 64 * 128 * 256 floats, past the
+    4,194,304 of the buffer -- also with the operator's sequential switch set,
+    which the no-allocation entry point does not read."""
+    monkeypatch.setenv("YUF_ROSA_SEGMENTED", "0")
     lib = _lib.lib()
     dummy = 256  # never dereferenced: the call returns before any device work
-    rc = lib.yuf_rosa_scan_f32_noalloc(64, 8192, 256, *([dummy] * 9))
+    rc = lib.yuf_rosa_scan_f32_noalloc(64, 8192, 256, *([dummy] * 8), None)
     assert rc == -1 and "static buffer" in lib.yuf_last_error().decode()

@@ -76,8 +76,13 @@ def _corrupt(path, tmp_path, mutate):
     return out
 
 
-@pytest.mark.parametrize("case", ["magic", "version", "truncated", "extra", "json", "format", "shape"])
+@pytest.mark.parametrize("case", ["magic", "version", "truncated", "extra", "json", "format", "shape", "no_tie",
+                                  "no_dropout", "no_midi", "midi_fields", "small_vocab", "no_header_version"])
 def test_cpp_loader_rejects_malformed_files(tiny_yuf, tmp_path, case):
+    """The rejections of vulkan/src/checkpoint.rs:90-149: magic, version, size,
+    JSON, format; serde's required fields (tie_embeddings, dropout, the midi
+    header, the header's version, :14-24, :58-80); and ModelConfig::validate's
+    vocab_size >= d_model (:44-46)."""
     path = tiny_yuf[0]
     header_len = struct.unpack("<Q", path.read_bytes()[8:16])[0]
 
@@ -95,6 +100,13 @@ def test_cpp_loader_rejects_malformed_files(tiny_yuf, tmp_path, case):
         "json": lambda d: d[:16] + b"{" * 3 + d[19:],
         "format": lambda d: rewrite_header(d, lambda h: h.update(format="other")),
         "shape": lambda d: rewrite_header(d, lambda h: h["tensors"][0].update(shape=[1, 2])),
+        "no_tie": lambda d: rewrite_header(d, lambda h: h["model_config"].pop("tie_embeddings")),
+        "no_dropout": lambda d: rewrite_header(d, lambda h: h["model_config"].pop("dropout")),
+        "no_midi": lambda d: rewrite_header(d, lambda h: h.pop("midi")),
+        "midi_fields": lambda d: rewrite_header(d, lambda h: h["midi"].pop("tokenization")),
+        "small_vocab": lambda d: rewrite_header(d, lambda h: h["model_config"].update(
+            vocab_size=h["model_config"]["d_model"] - 1)),
+        "no_header_version": lambda d: rewrite_header(d, lambda h: h.pop("version")),
     }[case]
     bad = _corrupt(path, tmp_path, mutate)
     with pytest.raises(YufError) as err:

@@ -37,11 +37,15 @@ def test_noalloc_matches_allocating_operator(shapes):
         np.testing.assert_array_equal(got[1], ref[1])
 
 
-def test_noalloc_sequential_shape_and_rejection():
+def test_noalloc_sequential_shape_and_rejection(monkeypatch):
+    # The capacity check must hold whatever the operator's env switch says.
+    monkeypatch.setenv("YUF_ROSA_SEGMENTED", "0")
     ref = _run(lib().yuf_rosa_scan_f32, 2, 100, 96, seed=3)  # T % 64 != 0: the sequential scan
     got = _run(lib().yuf_rosa_scan_f32_noalloc, 2, 100, 96, seed=3)
     np.testing.assert_array_equal(got[0], ref[0])
     np.testing.assert_array_equal(got[1], ref[1])
     x = torch.zeros(8, device="cuda")
-    rc = lib().yuf_rosa_scan_f32_noalloc(64, 8192, 256, *([x.data_ptr()] * 9))
+    # Rejected on the host before any launch: the buffers are never touched,
+    # and the stream is the default one (None), never a data pointer.
+    rc = lib().yuf_rosa_scan_f32_noalloc(64, 8192, 256, *([x.data_ptr()] * 8), None)
     assert rc == -1 and "static buffer" in lib().yuf_last_error().decode()

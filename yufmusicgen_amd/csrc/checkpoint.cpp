@@ -235,6 +235,9 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
     const json::Value *fmt = root.get("format");
     if (!fmt || fmt->kind != json::Value::String || fmt->str != "yufmusicgen-checkpoint")
         return fail(YUF_ERR_FORMAT, "unexpected .yuf payload format");
+    long long hdr_version = 0;
+    if (!get_int(&root, "version", hdr_version) || hdr_version < 0)
+        return fail(YUF_ERR_FORMAT, "header has no integer version field");
     const json::Value *mc = root.get("model_config");
     long long vocab, d, layers, heads, hs, rosa;
     if (!get_int(mc, "vocab_size", vocab) || !get_int(mc, "d_model", d) || !get_int(mc, "n_layers", layers) ||
@@ -243,20 +246,30 @@ int load_checkpoint(const char *path, Checkpoint &ck) {
     ModelShape &s = ck.shape;
     s.vocab = (int)vocab; s.d = (int)d; s.layers = (int)layers; s.heads = (int)heads; s.head_size = (int)hs;
     s.rosa = (int)rosa;
+    // Required fields and checks of the Rust loader: ModelConfig and MidiHeader
+    // are deserialized without defaults (vulkan/src/checkpoint.rs:14-24,
+    // :58-80), then ModelConfig::validate (:33-47) runs.
     const json::Value *tie = mc->get("tie_embeddings");
-    s.tie = !tie || tie->kind != json::Value::Bool || tie->b;
+    if (!tie || tie->kind != json::Value::Bool) return fail(YUF_ERR_FORMAT, "model_config.tie_embeddings must be a bool");
+    s.tie = tie->b;
     const json::Value *drop = mc->get("dropout");
-    s.dropout = drop && drop->kind == json::Value::Number ? (float)drop->num : 0.0f;
+    if (!drop || drop->kind != json::Value::Number) return fail(YUF_ERR_FORMAT, "model_config.dropout must be a number");
+    s.dropout = (float)drop->num;
     if (s.d != s.heads * s.head_size)
         return fail(YUF_ERR_FORMAT, "d_model " + std::to_string(s.d) + " must equal n_heads * head_size");
     if (s.d < 32 || s.layers < 1) return fail(YUF_ERR_FORMAT, "model is too small to be useful");
-    if (s.vocab < 1 || s.rosa < 1) return fail(YUF_ERR_FORMAT, "vocab_size and rosa_size must be positive");
+    if (s.rosa < 1) return fail(YUF_ERR_FORMAT, "rosa_size must be positive");
+    if (s.vocab < s.d)
+        return fail(YUF_ERR_FORMAT, "vocab_size " + std::to_string(s.vocab) + " looks wrong for d_model " +
+                                        std::to_string(s.d));
     const json::Value *midi = root.get("midi");
-    long long mo = 260, mv = 0;
-    if (midi) {
-        get_int(midi, "midi_offset", mo);
-        get_int(midi, "midi_vocab_size", mv);
-    }
+    long long mo = 0, mv = 0;
+    const json::Value *tok = midi ? midi->get("tokenization") : nullptr;
+    const json::Value *mvocab = midi ? midi->get("vocab") : nullptr;
+    if (!midi || midi->kind != json::Value::Object || !tok || tok->kind != json::Value::String ||
+        !get_int(midi, "midi_offset", mo) || !get_int(midi, "midi_vocab_size", mv) || mo < 0 || mv < 0 || !mvocab ||
+        mvocab->kind != json::Value::Array)
+        return fail(YUF_ERR_FORMAT, "midi header needs tokenization, midi_offset, midi_vocab_size and vocab");
     s.midi_offset = (int)mo;
     s.midi_vocab = (int)mv;
 

@@ -661,6 +661,20 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         G = std::min(G, n);
         while (G > 1 && (size_t)(n / G) * tc < 256) --G;
         if (G > 1) ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
+        // Join every side stream that waited on the fork back into e.stream,
+        // on the error paths too: the next call's token copy and workspace
+        // writes on e.stream must not overtake a side stream's kernels.
+        int forked = 0;
+        auto join_forked = [&]() -> hipError_t {
+            hipError_t first = hipSuccess;
+            for (int g = 1; g <= forked; ++g) {
+                hipError_t err = hipEventRecord(e.join[g - 1], e.side[g - 1]);
+                if (err == hipSuccess) err = hipStreamWaitEvent(e.stream, e.join[g - 1], 0);
+                if (first == hipSuccess) first = err;
+            }
+            forked = 0;
+            return first;
+        };
         // Last-position logits of a split batch: the parts gather their last
         // rows and one LM head runs over all of them after the join (the same
         // kernel, so the same values, as for the whole batch in one part).
@@ -672,7 +686,14 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
         for (int g = 0; g < G; ++g) {
             const int s0 = (int)((long long)n * g / G), s1 = (int)((long long)n * (g + 1) / G);
             hipStream_t st = g == 0 ? e.stream : e.side[g - 1];
-            if (g > 0) ENG_TRY(hipStreamWaitEvent(st, e.fork, 0), "fork wait");
+            if (g > 0) {
+                const hipError_t err = hipStreamWaitEvent(st, e.fork, 0);
+                if (err != hipSuccess) {
+                    (void)join_forked();
+                    return hip_fail(err, "fork wait");
+                }
+                forked = g;
+            }
             acts[g] = act_at(e, st, s0, tc);
             acts[g].bad = flag_for(e, tokens_dev);
             lgs[g] = logits_dev;
@@ -688,14 +709,14 @@ int prefill_impl(Engine &e, int n, int T, const int32_t *tokens_dev, float *logi
             const int l1 = G > 1 ? std::min(l + 1, layers) : layers;
             for (int g = 0; g < G; ++g) {
                 const int rc = forward_pass(e, acts[g], ns[g], tc, lgs[g], chunk_mode, T, t0, l, l1);
-                if (rc != YUF_OK) return rc;
+                if (rc != YUF_OK) {
+                    (void)join_forked();
+                    return rc;
+                }
             }
             if (l1 == layers) break;
         }
-        for (int g = 1; g < G; ++g) {
-            ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
-            ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
-        }
+        ENG_TRY(join_forked(), "join");
         if (head_after) {
             const Act a0 = act_at(e, e.stream, 0, tc);
             const int rc = ln_gemm(e, e.stream, n, e.s.vocab, e.s.d, tc > 1 ? e.hl : e.h, e.s.d, e.ln_fin_w,
@@ -749,7 +770,13 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
     if (!e.use_graphs) return prefill_impl(e, n, 1, tokens_dev, logits_dev, YUF_LOGITS_LAST);
     // Measured on MI355X (0.1B model, 64 streams): one group 0.975 ms per step,
     // two 0.953, three 1.068 (21-row groups: no whole tiles), four 1.030.
-    const int G = e.branches > 0 ? std::max(1, std::min(e.branches, n)) : (n >= 64 && n % 32 == 0 ? 2 : 1);
+    // Groups run concurrently and share e.gemm_ws, the split-K workspace of
+    // short products, so they are used only when no decode product can take
+    // the split-K path (every K a multiple of the decode kernel's k step).
+    const int kq = e.w_h ? 8 : 4;
+    const bool no_split_k = e.s.d % kq == 0 && e.s.low_rank % kq == 0 && e.s.rosa % kq == 0;
+    int G = e.branches > 0 ? std::max(1, std::min(e.branches, n)) : (n >= 64 && n % 32 == 0 ? 2 : 1);
+    if (!no_split_k) G = 1;
     auto group = [&](int g) { return std::make_pair((int)((long long)n * g / G), (int)((long long)n * (g + 1) / G)); };
     auto stream_of = [&](int g) { return g == 0 ? e.stream : e.side[g - 1]; };
     if (!(e.step_exec[0] && e.step_n == n && e.step_tok == tokens_dev && e.step_logits == logits_dev)) {
@@ -793,12 +820,19 @@ int step_impl(Engine &e, int n, const int32_t *tokens_dev, float *logits_dev) {
         return YUF_OK;
     }
     ENG_TRY(hipEventRecord(e.fork, e.stream), "fork record");
-    for (int g = 1; g < G; ++g) ENG_TRY(hipStreamWaitEvent(e.side[g - 1], e.fork, 0), "fork wait");
-    for (int g = 0; g < G; ++g) ENG_TRY(hipGraphLaunch(e.step_exec[g], stream_of(g)), "graph launch");
-    for (int g = 1; g < G; ++g) {
-        ENG_TRY(hipEventRecord(e.join[g - 1], e.side[g - 1]), "join record");
-        ENG_TRY(hipStreamWaitEvent(e.stream, e.join[g - 1], 0), "join wait");
+    // Every side stream that waited on the fork is joined back into e.stream,
+    // also when a later launch fails.
+    int forked = 0;
+    hipError_t err = hipSuccess;
+    for (int g = 1; g < G && err == hipSuccess; ++g)
+        if ((err = hipStreamWaitEvent(e.side[g - 1], e.fork, 0)) == hipSuccess) forked = g;
+    for (int g = 0; g < G && err == hipSuccess; ++g) err = hipGraphLaunch(e.step_exec[g], stream_of(g));
+    for (int g = 1; g <= forked; ++g) {
+        hipError_t je = hipEventRecord(e.join[g - 1], e.side[g - 1]);
+        if (je == hipSuccess) je = hipStreamWaitEvent(e.stream, e.join[g - 1], 0);
+        if (err == hipSuccess) err = je;
     }
+    if (err != hipSuccess) return hip_fail(err, "step branches");
     ENG_TRY(hipGraphLaunch(e.step_exec[G], e.stream), "graph launch");
     return YUF_OK;
 }

@@ -627,7 +627,9 @@ int noalloc_scratch(float **out) {
 
 // The operator: argument checks, then the segmented form (scratch from the
 // growing per-stream buffer, or from `scratch` when noalloc) or the
-// sequential chunked scan (no scratch).
+// sequential chunked scan (no scratch).  The no-allocation variant does not
+// read YUF_ROSA_SEGMENTED: its scratch capacity is checked on every call that
+// can take the segmented form, before any launch, whatever the switch says.
 int rosa_operator(int B, int T, int D, const float *cand, const float *write, const float *read_raw,
                   const float *decay, const float *direction, const float *memory_in, float *memory_out,
                   float *read_out, void *stream, bool noalloc) {
@@ -642,7 +644,7 @@ int rosa_operator(int B, int T, int D, const float *cand, const float *write, co
     p.memory_in = memory_in; p.memory_out = memory_out; p.read_out = read_out;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     hipError_t err;
-    if (B > 0 && rosa_segmented_ok(T, D, kOpRosaSeg) && !op_rosa_sequential()) {
+    if (B > 0 && rosa_segmented_ok(T, D, kOpRosaSeg) && (noalloc || !op_rosa_sequential())) {
         // Segmented form (as the engine's prefill): A^L on the device, then
         // segments from zero, the carry chain, and segments from their starts.
         float *buf = nullptr;
