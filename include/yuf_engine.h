@@ -333,7 +333,8 @@ int yuf_generation_mask(const float *logits, int V, int index, int midi_offset, 
 
 /* Device sampling for n streams at once (no logits copy to the host):
  * temperature <= 0 -> argmax; otherwise the top_k in [1, 64] largest scaled
- * logits, softmax over them and a draw argmax p / q with q = -log u, u from a
+ * logits (top_k 0 or >= V: all of them, V <= 24576), softmax over them and a
+ * draw argmax p / q with q = -log u, u from a
  * counter-based generator keyed by (seed, counter, stream, token id) -- the
  * distribution of torch.multinomial, not its stream.  logits_dev [n, V];
  * tokens_dev [n] int32.  yuf_sample_device_masked(..., midi_offset = -1,
@@ -353,13 +354,17 @@ int yuf_sample_device(int n, int V, const float *logits_dev, float temperature, 
  *     mask.
  *   draw: temperature <= 0 -> the first maximum of the masked logits;
  *     otherwise top_k in [1, 64] (the k largest masked logits / temperature),
+ *     or top_k = 0 (or >= V) for the whole vocabulary -- the reference's
+ *     sampling, temperature 1 and top_p 0.95 with no top-k
+ *     (cli/generate.py:39-56; vulkan/src/main.rs:78-82), for V <= 24576 --
  *     then top_p and the draw exactly as yuf_sample computes them.
- *     exp_draws_dev (device [n, top_k] float) and first_zero_dev (device [n]
- *     int32), filled from each stream's generator by yuf_rng_exp_draws, make
- *     the token equal yuf_sample(masked logits, temperature, top_p, top_k,
- *     rng) for the same generator state; with exp_draws_dev NULL the
- *     counter-based draws of yuf_sample_device are used (first_zero_dev
- *     ignored).
+ *     exp_draws_dev (device [n, top_k] float, or [n, V] when top_k = 0 or
+ *     >= V) and first_zero_dev (device [n] int32; not read when top_k = 0 or
+ *     >= V), filled from each stream's generator by yuf_rng_exp_draws(rng, V,
+ *     k, ...) with k the number of draws per stream, make the token equal
+ *     yuf_sample(masked logits, temperature, top_p, top_k, rng) for the same
+ *     generator state; with exp_draws_dev NULL the counter-based draws of
+ *     yuf_sample_device are used (first_zero_dev ignored).
  * Asynchronous on `stream`; tokens_dev [n] int32. */
 int yuf_sample_device_masked(int n, int V, const float *logits_dev, float temperature, float top_p,
                              int top_k, int midi_offset, int eos_id, int min_before_eos, int index,

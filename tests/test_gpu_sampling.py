@@ -146,6 +146,97 @@ def test_exact_mode_with_heavy_ties_takes_the_radix_path():
         np.testing.assert_array_equal(tokens.cpu().numpy(), np.array(expect), err_msg=f"step {step}")
 
 
+@pytest.mark.parametrize("temperature,top_p,scale", [(1.0, 0.95, 3.0), (1.0, 0.95, 0.05), (0.7, 0.5, 1.0),
+                                                     (1.5, 0.99, 8.0), (1.0, 1.0, 0.5), (1.0, 0.0, 1.0)])
+@pytest.mark.parametrize("masked", [True, False])
+def test_full_vocab_exact_mode_equals_host_sampler(temperature, top_p, scale, masked):
+    """The reference's own parameters (temperature 1, top_p 0.95, no top-k:
+    cli/generate.py:39-56, sampler.rs:131-256) on the device: top_k = 0 sorts
+    all V logits.  64 rows of 20480, three draws per row from its own
+    generator (all V Exp(1) draws of one host sample as the exact-mode input):
+    the device token equals yuf_sample's, top_k 0, on the masked logits.
+    Scale 0.05 is the near-flat case of the random-init model, whose nucleus
+    holds most of the vocabulary."""
+    print(f"full exact T={temperature} top_p={top_p} scale={scale} mask={masked}", flush=True)
+    n, vocab = 64, 20480
+    x = _rows(n, vocab, seed=int(scale * 10) + int(masked), scale=scale)
+    logits = torch.from_numpy(x).cuda()
+    tokens = torch.empty(n, dtype=torch.int32, device="cuda")
+    index = np.where(np.arange(n) % 2 == 0, 3, 20).astype(np.int32)
+    index_dev = torch.from_numpy(index).cuda()
+    host = [Mt19937(500 + s) for s in range(n)]
+    dev = [g.copy() for g in host]
+    for step in range(3):
+        q, _ = _exact_draws(dev, vocab, vocab)
+        sample_device_masked(logits, tokens, temperature, top_p, 0, mask=MASK if masked else None,
+                             index=index_dev, exp_draws=q)
+        torch.cuda.synchronize()
+        got = tokens.cpu().numpy()
+        expect = []
+        for s in range(n):
+            row = generation_mask(x[s], int(index[s]), MASK["blocked"]) if masked else x[s]
+            expect.append(sample_token(row, temperature, top_p, host[s], top_k=0))
+        np.testing.assert_array_equal(got, np.array(expect), err_msg=f"step {step}")
+        x = np.roll(x, 7, axis=1)
+        logits.copy_(torch.from_numpy(x))
+
+
+@pytest.mark.parametrize("vocab", [300, 1000, 24576])
+def test_full_vocab_edge_rows(vocab):
+    """Ties (values rounded to 0.1), -0.0 beside +0.0, a fully -inf row, rows
+    with a single allowed id, V not a multiple of 16 or of 1024, the largest
+    V, and top_k >= V (the same path): against yuf_sample, two draws each."""
+    rng = np.random.default_rng(vocab)
+    n = 8
+    x = np.round(rng.standard_normal((n, vocab)), 1).astype(np.float32)
+    x[1, ::2] = -0.0
+    x[1, 1::2] = 0.0
+    x[2] = -np.inf
+    x[3] = -np.inf
+    x[3, vocab // 3] = 1.0
+    x[4] = (rng.standard_normal(vocab) * 40.0).astype(np.float32)  # tiny tail probabilities
+    x[5] = 0.0  # all equal
+    logits = torch.from_numpy(x).cuda()
+    tokens = torch.empty(n, dtype=torch.int32, device="cuda")
+    for top_k, top_p in ((0, 0.95), (vocab, 0.8), (0, 1.0), (vocab + 5, 0.3)):
+        host = [Mt19937(90 + s) for s in range(n)]
+        dev = [g.copy() for g in host]
+        for step in range(2):
+            q, _ = _exact_draws(dev, vocab, vocab)
+            sample_device_masked(logits, tokens, 0.9, top_p, top_k, exp_draws=q)
+            torch.cuda.synchronize()
+            expect = [sample_token(x[s], 0.9, top_p, host[s], top_k=top_k) for s in range(n)]
+            np.testing.assert_array_equal(tokens.cpu().numpy(), np.array(expect),
+                                          err_msg=f"top_k={top_k} top_p={top_p} step {step}")
+
+
+def test_full_vocab_counter_mode_stays_in_the_nucleus():
+    """Counter draws (no host work): every token lies in the host's nucleus of
+    the masked row, and a near-flat row spreads over many ids."""
+    n, vocab = 16, 20480
+    x = _rows(n, vocab, seed=21, scale=1.0)
+    x[0] = np.random.default_rng(5).standard_normal(vocab).astype(np.float32) * 0.05
+    logits = torch.from_numpy(x).cuda()
+    tokens = torch.empty(n, dtype=torch.int32, device="cuda")
+    nuclei = []
+    for s in range(n):
+        row = generation_mask(x[s], 20, MASK["blocked"]).astype(np.float64)
+        order = sorted(range(vocab), key=lambda i: (-row[i], i))
+        pr = np.exp(row[order] - row[order[0]])
+        pr /= pr.sum()
+        cum = np.cumsum(pr)
+        nuclei.append(set(np.array(order)[(cum - pr) <= 0.95 + 1e-6].tolist()))
+    seen = set()
+    for c in range(30):
+        sample_device_masked(logits, tokens, 1.0, 0.95, 0, mask=MASK, index=20, seed=11, counter=c)
+        torch.cuda.synchronize()
+        got = tokens.cpu().numpy()
+        for s in range(n):
+            assert int(got[s]) in nuclei[s], (s, int(got[s]))
+        seen.add(int(got[0]))
+    assert len(seen) > 20
+
+
 def test_masked_sampler_rejects_bad_arguments():
     from yufmusicgen_amd._lib import YufError
 
@@ -157,3 +248,6 @@ def test_masked_sampler_rejects_bad_arguments():
         sample_device_masked(logits, tokens, 1.0, 1.0, 8, mask=dict(eos_id=300), index=20)
     with pytest.raises(YufError):
         sample_device_masked(logits, tokens, 1.0, 1.0, 65)
+    wide = torch.zeros(1, 24577, device="cuda")  # past the full-vocabulary path's limit
+    with pytest.raises(YufError):
+        sample_device_masked(wide, tokens[:1], 1.0, 0.95, 0)

@@ -140,3 +140,54 @@ def test_rng_copy_is_independent():
     rng.next_u32()
     twin = rng.copy()
     assert [rng.next_u32() for _ in range(700)] == [twin.next_u32() for _ in range(700)]
+
+
+def _host_probs(x):
+    """The host sampler's first softmax over a sorted row (float exps of the
+    double exponential, the 16-lane sum, one reciprocal)."""
+    mx = x[0]
+    e = np.exp((x - mx).astype(np.float64)).astype(np.float32)
+    acc = np.zeros(16, np.float32)
+    for i in range(0, e.size, 16):
+        chunk = e[i:i + 16]
+        acc[:chunk.size] = (acc[:chunk.size] + chunk).astype(np.float32)
+    for half in (8, 4, 2, 1):
+        acc[:half] = (acc[:half] + acc[half:2 * half]).astype(np.float32)
+    return (e * (np.float32(1.0) / acc[0])).astype(np.float32)
+
+
+@pytest.mark.parametrize("scale,top_p", [(3.0, 0.95), (0.05, 0.95), (1.0, 0.5), (8.0, 0.99), (0.5, 1.0),
+                                         (20.0, 0.9)])
+def test_full_vocab_cut_by_exact_prefix_equals_sequential_double_sum(scale, top_p):
+    """The device's full-vocabulary top-p cut (yuf_sample_device_masked with
+    top_k = 0) replaces the host's sequential double cumulative sum by an
+    integer prefix sum of p * 2^53 wherever every p so far is a multiple of
+    2^-53 and the sum is at most 1 -- there each double addition is exact --
+    and decides other positions by a 2^-20 bound on an approximate prefix.
+    Checked here against the sequential loop of yuf_sample itself: the exact
+    region's sums are bit-equal, and every decision the kernel takes without
+    its sequential fallback equals the host's."""
+    rng = np.random.default_rng(int(scale * 100) + int(top_p * 1000))
+    for trial in range(20):
+        x = -np.sort(-(rng.standard_normal(20480) * scale).astype(np.float32))
+        p = _host_probs(x)
+        cum = np.cumsum(p.astype(np.float64))  # sequential, as the host loop
+        host_drop = (cum.astype(np.float32) - p) > np.float32(top_p)
+        t = p.astype(np.float64) * 2.0**53
+        exact = (t == np.floor(t)) & (t <= 2.0**62)
+        fb = int(np.argmin(exact)) if not exact.all() else p.size
+        nsum = np.cumsum(np.where(exact, t, 0).astype(np.uint64))
+        ok = (np.arange(p.size) < fb) & (nsum <= np.uint64(2**53))
+        assert ok[:100].all() or scale >= 8.0  # the exact region covers the head of the order
+        np.testing.assert_array_equal(cum[ok], nsum[ok].astype(np.float64) * 2.0**-53)
+        dev_drop = (nsum.astype(np.float64) * 2.0**-53).astype(np.float32) - p > np.float32(top_p)
+        # The kernel's approximate prefix (a block scan, another summation
+        # order): the sequential sum moved by up to 2^-37.
+        aprev = np.concatenate([[0.0], cum[:-1]]) + rng.uniform(-2.0**-37, 2.0**-37, p.size)
+        certain_drop = aprev > top_p + 2.0**-20
+        certain_keep = aprev < top_p - 2.0**-20
+        decided = ok | certain_drop | certain_keep
+        dev_drop = np.where(ok, dev_drop, certain_drop)
+        np.testing.assert_array_equal(dev_drop[decided], host_drop[decided])
+        if top_p < 1.0:
+            assert decided.all(), "fallback needed below top_p = 1"

@@ -424,10 +424,407 @@ __global__ void __launch_bounds__(NTH) sample_kernel(SampleParams p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Full vocabulary (top_k = 0, or top_k >= V): the reference's own parameters
+// (temperature 1, top_p 0.95, no top-k: cli/generate.py:39-56,
+// vulkan/src/sampler.rs:131-256).  The host sampler sorts all V scaled logits
+// (stable, descending) and its softmax sums run over all of them in its
+// 16-lane order, so every value's position matters.  One workgroup of 1024
+// threads per stream:
+//   1. mask + scale, then a stable LSD radix sort of (key, token id) in LDS:
+//      4-bit digits, eight passes (a pass whose digit is the same for every
+//      value is skipped); element e of a pass is handled by thread e % 1024
+//      in round e / 1024, so a ballot ranks it among its wave's equal digits
+//      and an exclusive scan over (digit, round, wave) counts places it;
+//   2. e_i = exp(x_i - max) rounded once to float, their sum by 16 lanes in
+//      the host's order, p_i = e_i * (1 / sum);
+//   3. the cut (float)cum_i - p_i > top_p with cum the host's sequential
+//      double sum: while every p is a multiple of 2^-53 and the running sum
+//      stays <= 1, each double addition is exact, so cum_i is the integer
+//      prefix sum of p * 2^53 (one block scan); elsewhere a position whose
+//      approximate prefix is more than 2^-20 away from top_p is decided by
+//      the bound, and any other position makes one lane redo the host's
+//      sequential loop up to it;
+//   4. the second softmax over the kept positions (the maximum is position
+//      0's, which the cut always keeps for top_p >= 0) and the draw argmax
+//      p / q over all V positions, q the host's Exp(1) draws (exact mode,
+//      [n, V]) or the counter hash.
+constexpr int kFullThreads = 1024;
+constexpr int kFullWaves = kFullThreads / 64;
+constexpr int kFullMaxV = 24576;
+constexpr int kFullMaxRounds = kFullMaxV / kFullThreads;
+constexpr uint16_t kDropBit = 0x8000;  // top-p cut flag in the id array (ids < 32768)
+
+// Ascending keys = the host's descending order of values; -0.0 counts as +0.0
+// (the host's comparison cannot tell them apart).
+__device__ __forceinline__ uint32_t desc_key(float x) { return ~order_key(x == 0.0f ? 0.0f : x); }
+
+__device__ __forceinline__ float from_desc_key(uint32_t k) {
+    const uint32_t o = ~k;
+    return __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T x, int lane) {
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const T y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+    }
+    return x;
+}
+
+// Exclusive scan of one value per thread in thread order (sh: kFullWaves
+// slots).  Ends with a barrier, so sh can be reused at once.
+template <typename T>
+__device__ __forceinline__ T block_excl_scan(T x, T *sh, int lane, int wave) {
+    const T incl = wave_incl_scan(x, lane);
+    T excl = __shfl_up(incl, 1);
+    if (lane == 0) excl = T(0);
+    if (lane == 63) sh[wave] = incl;
+    __syncthreads();
+    T base = T(0);
+    for (int w = 0; w < wave; ++w) base += sh[w];
+    __syncthreads();
+    return base + excl;
+}
+
+// Sum of e[0..n) in the host sampler's order (16 lane accumulators over
+// consecutive chunks of 16, then halves folded 8 / 4 / 2 / 1), skipping
+// positions whose id carries the drop flag when `cut`.  Lanes 0..15 of one
+// wave; lane 0 returns the sum.
+__device__ __forceinline__ float sum16_lds(const float *e, const uint16_t *ids, int n, bool cut, int lane) {
+    float acc = 0.0f;
+    if (lane < 16) {
+        int i = lane;
+        for (; i + 7 * 16 < n; i += 8 * 16) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                v[u] = e[i + 16 * u];
+                if (cut && (ids[i + 16 * u] & kDropBit)) v[u] = 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += v[u];
+        }
+        for (; i < n; i += 16) acc += (cut && (ids[i] & kDropBit)) ? 0.0f : e[i];
+    }
+#pragma unroll
+    for (int half = 8; half >= 1; half >>= 1) {
+        const float o = __shfl_down(acc, half);
+        if (lane < half) acc = acc + o;
+    }
+    return acc;
+}
+
+__global__ void __launch_bounds__(kFullThreads) sample_full_kernel(SampleParams p) {
+    __shared__ uint32_t skey[kFullMaxV];  // sort keys; after the sort, e_i as float bits
+    __shared__ uint16_t sidx[kFullMaxV];  // token ids; kDropBit once cut by top-p
+    // Digit counts, then their offsets, per (digit, round, wave); before the
+    // sort, the blocked-id bitmap of the generation mask.
+    __shared__ uint32_t scnt32[16 * kFullMaxRounds * kFullWaves / 2];
+    __shared__ uint64_t sh_u64[kFullWaves];
+    __shared__ double sh_f64[kFullWaves];
+    __shared__ int sh_int[kFullWaves], sh_int2[kFullWaves];
+    __shared__ float sh_flt[kFullWaves];
+    __shared__ float sh_sum;
+    static_assert(kSampleMaskWords <= 16 * kFullMaxRounds * kFullWaves / 2, "bitmap fits the count array");
+    uint16_t *scnt = reinterpret_cast<uint16_t *>(scnt32);
+    float *se = reinterpret_cast<float *>(skey);
+
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int V = p.V;
+    const int R = (V + kFullThreads - 1) / kFullThreads;
+    const float *row = p.logits + (size_t)s * V;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+
+    // 1. Generation mask and temperature (as sample_kernel).
+    uint32_t *blocked_bits = scnt32;
+    const bool masked = p.midi_offset >= 0;
+    const int mo = p.midi_offset;
+    const bool eos_ok = masked && (p.index ? p.index[s] : p.index_all) >= p.min_before_eos;
+    if (masked) {
+        for (int w = tid; w < kSampleMaskWords; w += kFullThreads) blocked_bits[w] = 0u;
+        __syncthreads();
+        for (int j = tid; j < p.n_blocked; j += kFullThreads) {
+            const int raw = p.blocked[j];
+            atomicOr(&blocked_bits[raw >> 5], 1u << (raw & 31));
+        }
+        __syncthreads();
+    }
+    for (int r = 0; r < R; ++r) {
+        const int i = r * kFullThreads + tid;
+        uint32_t key = 0xffffffffu;  // padding: after every value
+        if (i < V) {
+            float x = row[i];
+            if (masked) {
+                const int raw = i - mo;
+                const bool blocked =
+                    raw >= 0 && raw < 32 * kSampleMaskWords && ((blocked_bits[raw >> 5] >> (raw & 31)) & 1u);
+                const bool allowed = (raw >= 0 && !blocked) || (i == p.eos_id && eos_ok);
+                x = allowed ? x : -INFINITY;
+            }
+            key = desc_key(x / p.temperature);
+        }
+        skey[i] = key;
+        sidx[i] = (uint16_t)i;
+    }
+    __syncthreads();
+
+    // Stable LSD radix sort of (key, id), 4 bits per pass.
+    const int n_cnt = 16 * R * kFullWaves;
+    const int per = (n_cnt + kFullThreads - 1) / kFullThreads;
+    for (int shift = 0; shift < 32; shift += 4) {
+        uint32_t kr[kFullMaxRounds], ir[kFullMaxRounds];
+#pragma unroll
+        for (int r = 0; r < kFullMaxRounds; ++r)
+            if (r < R) {
+                kr[r] = skey[r * kFullThreads + tid];
+                ir[r] = sidx[r * kFullThreads + tid];
+            }
+#pragma unroll
+        for (int r = 0; r < kFullMaxRounds; ++r)
+            if (r < R) {
+                const uint32_t dg = (kr[r] >> shift) & 15u;
+                uint64_t bal[4];
+                uint64_t same = ~0ull;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    bal[b] = __ballot((dg >> b) & 1u);
+                    same &= ((dg >> b) & 1u) ? bal[b] : ~bal[b];
+                }
+                ir[r] |= (uint32_t)__popcll(same & lt_mask) << 16;
+                if (lane < 16) {
+                    uint64_t m = ~0ull;
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) m &= ((lane >> b) & 1) ? bal[b] : ~bal[b];
+                    scnt[(lane * R + r) * kFullWaves + wave] = (uint16_t)__popcll(m);
+                }
+            }
+        __syncthreads();
+        // Exclusive scan of the counts in (digit, round, wave) order.
+        {
+            int loc[8];
+            int tot = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = tid * per + j;
+                loc[j] = (j < per && c < n_cnt) ? (int)scnt[c] : 0;
+                tot += loc[j];
+            }
+            int base = block_excl_scan(tot, sh_int, lane, wave);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int c = tid * per + j;
+                if (j < per && c < n_cnt) scnt[c] = (uint16_t)base;
+                base += loc[j];
+            }
+        }
+        __syncthreads();
+        // A digit that every element shares leaves the order unchanged.
+        bool trivial = false;
+        const int np = R * kFullThreads;
+        for (int d = 0; d < 16; ++d) {
+            const int lo = scnt[d * R * kFullWaves], hi = d < 15 ? (int)scnt[(d + 1) * R * kFullWaves] : np;
+            trivial |= hi - lo == np;
+        }
+        if (!trivial) {
+#pragma unroll
+            for (int r = 0; r < kFullMaxRounds; ++r)
+                if (r < R) {
+                    const uint32_t dg = (kr[r] >> shift) & 15u;
+                    const int pos = (int)scnt[(dg * R + r) * kFullWaves + wave] + (int)(ir[r] >> 16);
+                    skey[pos] = kr[r];
+                    sidx[pos] = (uint16_t)(ir[r] & 0xffffu);
+                }
+        }
+        __syncthreads();
+    }
+
+    // 2. First softmax.  Thread t owns the R consecutive positions from t R.
+    const float mx = from_desc_key(skey[0]);
+    __syncthreads();
+    const int p0 = tid * R;
+#pragma unroll
+    for (int j = 0; j < kFullMaxRounds; ++j)
+        if (j < R) {
+            const int pos = p0 + j;
+            se[pos] = pos < V ? exp_rn(from_desc_key(skey[pos]) - mx) : 0.0f;
+        }
+    __syncthreads();
+    if (wave == 0) {
+        const float sum = sum16_lds(se, sidx, V, false, lane);
+        if (lane == 0) sh_sum = sum;
+    }
+    __syncthreads();
+    const float inv = 1.0f / sh_sum;
+
+    // 3. The top-p cut.  Exact prefix sums of p * 2^53 where every p so far is
+    // a multiple of 2^-53; approximate double prefix sums for the bounds.
+    uint64_t nloc = 0;
+    double aloc = 0.0;
+    int first_inexact = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kFullMaxRounds; ++j)
+        if (j < R) {
+            const float pr = se[p0 + j] * inv;
+            const double t = (double)pr * 0x1p53;
+            const bool exact = t >= 0.0 && t <= 0x1p62 && t == floor(t);
+            if (exact) nloc += (uint64_t)t;
+            else first_inexact = min(first_inexact, p0 + j);
+            aloc += (double)pr;
+        }
+    const uint64_t nbase = block_excl_scan(nloc, sh_u64, lane, wave);
+    const double abase = block_excl_scan(aloc, sh_f64, lane, wave);
+    for (int off = 32; off >= 1; off >>= 1) first_inexact = min(first_inexact, __shfl_xor(first_inexact, off));
+    if (lane == 0) sh_int[wave] = first_inexact;
+    __syncthreads();
+    int fb = sh_int[0];
+    for (int w = 1; w < kFullWaves; ++w) fb = min(fb, sh_int[w]);
+    __syncthreads();
+    int last_uncertain = -1, last_kept = -1;
+    {
+        uint64_t nsum = nbase;
+        double asum = abase;  // approximate sum before position
+#pragma unroll
+        for (int j = 0; j < kFullMaxRounds; ++j)
+            if (j < R) {
+                const int pos = p0 + j;
+                if (pos >= V) continue;  // padding
+                const float pr = se[pos] * inv;
+                const double aprev = asum;
+                asum += (double)pr;
+                bool drop;
+                if (pos < fb) nsum += (uint64_t)((double)pr * 0x1p53);
+                if (pos < fb && nsum <= (1ull << 53)) {
+                    const double cum = (double)nsum * 0x1p-53;  // the host's running sum, exactly
+                    drop = (float)cum - pr > p.top_p;
+                } else if (aprev > (double)p.top_p + 0x1p-20) {
+                    drop = true;
+                } else if (aprev < (double)p.top_p - 0x1p-20) {
+                    drop = false;
+                } else {
+                    drop = false;
+                    last_uncertain = pos;
+                }
+                const uint16_t id = sidx[pos] & (uint16_t)~kDropBit;
+                sidx[pos] = drop ? (uint16_t)(id | kDropBit) : id;
+                if (!drop) last_kept = pos;
+            }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        last_uncertain = max(last_uncertain, __shfl_xor(last_uncertain, off));
+        last_kept = max(last_kept, __shfl_xor(last_kept, off));
+    }
+    if (lane == 0) {
+        sh_int[wave] = last_uncertain;
+        sh_int2[wave] = last_kept;
+    }
+    __syncthreads();
+    int lu = -1, lk = -1;
+    for (int w = 0; w < kFullWaves; ++w) {
+        lu = max(lu, sh_int[w]);
+        lk = max(lk, sh_int2[w]);
+    }
+    if (lu >= 0) {
+        // Undecided positions: the host's loop itself, up to the last of them.
+        __syncthreads();  // every thread has read sh_int / sh_int2
+        if (tid == 0) {
+            double cum = 0.0;
+            int kept = -1;
+            for (int pos = 0; pos <= lu && pos < V; ++pos) {
+                const float pr = se[pos] * inv;
+                cum += (double)pr;
+                const bool drop = (float)cum - pr > p.top_p;
+                const uint16_t id = sidx[pos] & (uint16_t)~kDropBit;
+                sidx[pos] = drop ? (uint16_t)(id | kDropBit) : id;
+                if (!drop) kept = pos;
+            }
+            sh_int[0] = kept;
+        }
+        __syncthreads();
+        lk = max(lk, sh_int[0]);
+        // Positions after lu keep their bounded decisions; the last kept one
+        // may now lie before lu: recount from the flags.
+        if (tid == 0) {
+            int k2 = -1;
+            for (int pos = min(V, kFullMaxV) - 1; pos >= 0; --pos)
+                if (!(sidx[pos] & kDropBit)) { k2 = pos; break; }
+            sh_int[1] = k2;
+        }
+        __syncthreads();
+        lk = sh_int[1];
+    }
+    __syncthreads();
+    if (lk < 0 || (sidx[0] & kDropBit)) {
+        // Everything cut (top_p < 0): the host's second softmax is NaN at every
+        // position and its draw keeps position 0.
+        if (tid == 0) p.tokens[s] = (int)(sidx[0] & (uint16_t)~kDropBit);
+        return;
+    }
+
+    // 4. Second softmax over the kept positions (same maximum, so the same
+    // exponentials), then the draw.
+    if (wave == 0) {
+        const float sum2 = sum16_lds(se, sidx, lk + 1, true, lane);
+        if (lane == 0) sh_sum = sum2;
+    }
+    __syncthreads();
+    const float inv2 = 1.0f / sh_sum;
+    int nan_pos = 0x7fffffff, best_pos = 0x7fffffff;
+    float best = -1.0f;
+#pragma unroll
+    for (int j = 0; j < kFullMaxRounds; ++j)
+        if (j < R) {
+            const int pos = p0 + j;
+            if (pos < V) {
+                const uint16_t raw = sidx[pos];
+                const float p2 = (raw & kDropBit) ? 0.0f : se[pos] * inv2;
+                float sc;
+                if (p.exp_draws) {
+                    sc = p2 / p.exp_draws[(size_t)s * V + pos];
+                } else {
+                    sc = p2 == 0.0f ? 0.0f : p2 / -logf(uniform01(p.seed, p.counter, s, raw & (uint16_t)~kDropBit));
+                }
+                if (isnan(sc)) nan_pos = min(nan_pos, pos);
+                else if (sc > best) { best = sc; best_pos = pos; }
+            }
+        }
+    for (int off = 32; off >= 1; off >>= 1) {
+        nan_pos = min(nan_pos, __shfl_xor(nan_pos, off));
+        const float ob = __shfl_xor(best, off);
+        const int op = __shfl_xor(best_pos, off);
+        if (ob > best || (ob == best && op < best_pos)) { best = ob; best_pos = op; }
+    }
+    if (lane == 0) {
+        sh_int[wave] = nan_pos;
+        sh_int2[wave] = best_pos;
+        sh_flt[wave] = best;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        int np_ = sh_int[0], bp = sh_int2[0];
+        float bs = sh_flt[0];
+        for (int w = 1; w < kFullWaves; ++w) {
+            np_ = min(np_, sh_int[w]);
+            if (sh_flt[w] > bs || (sh_flt[w] == bs && sh_int2[w] < bp)) { bs = sh_flt[w]; bp = sh_int2[w]; }
+        }
+        const int pos = np_ != 0x7fffffff ? np_ : bp;
+        p.tokens[s] = pos < V ? (int)(sidx[pos] & (uint16_t)~kDropBit) : 0;
+    }
+}
+
 }  // namespace
+
+bool sample_full_vocab(int top_k, int V) { return top_k == 0 || top_k >= V; }
 
 hipError_t launch_sample(const SampleParams &p, int n, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
+    if (p.temperature > 0.0f && sample_full_vocab(p.top_k, p.V)) {
+        if (p.V > kFullMaxV) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(sample_full_kernel, dim3(n), dim3(kFullThreads), 0, stream, p);
+        return hipGetLastError();
+    }
     if (p.temperature > 0.0f && (p.top_k < 1 || p.top_k > kMaxTopK)) return hipErrorInvalidValue;
     if (p.V <= kRegElems)
         hipLaunchKernelGGL((sample_kernel<kRegThreads, true>), dim3(n), dim3(kRegThreads), 0, stream, p);
@@ -442,8 +839,13 @@ namespace {
 int check_sample_args(int n, int V, const float *logits_dev, float temperature, int top_k, const int32_t *tokens_dev) {
     using namespace yuf;
     if (n < 0 || V <= 0) return fail(YUF_ERR_INVALID, "sample_device: bad sizes");
-    if (temperature > 0.0f && (top_k < 1 || top_k > 64))
-        return fail(YUF_ERR_INVALID, "sample_device: top_k must be in [1, 64] when temperature > 0");
+    if (temperature > 0.0f && sample_full_vocab(top_k, V)) {
+        if (V > kFullMaxV)
+            return fail(YUF_ERR_INVALID, "sample_device: the full-vocabulary path (top_k = 0 or >= V) needs V <= " +
+                                             std::to_string(kFullMaxV));
+    } else if (temperature > 0.0f && (top_k < 1 || top_k > 64)) {
+        return fail(YUF_ERR_INVALID, "sample_device: top_k must be 0 (all V), in [1, 64] or >= V when temperature > 0");
+    }
     if (n > 0 && (!logits_dev || !tokens_dev)) return fail(YUF_ERR_INVALID, "sample_device: null pointer");
     return YUF_OK;
 }

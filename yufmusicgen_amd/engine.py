@@ -292,7 +292,10 @@ def sample_device_masked(logits_dev, tokens_dev, temperature: float, top_p: floa
     min_before_eos=16, blocked=(...)) or None; ``index``: an int for every
     stream or an int32 GPU tensor [n]; ``exp_draws`` [n, top_k] float32 and
     ``first_zero`` [n] int32 GPU tensors (from ``Mt19937.exp_draws``) select
-    the exact mode, else the counter-based draws of ``seed`` / ``counter``."""
+    the exact mode, else the counter-based draws of ``seed`` / ``counter``.
+    ``top_k`` 0 (or >= V) samples over the whole vocabulary (V <= 24576), the
+    reference's top-p sampling; its exact mode takes all V draws,
+    ``exp_draws`` [n, V] from ``Mt19937.exp_draws(V, V)``."""
     import torch
 
     n, vocab = logits_dev.shape
