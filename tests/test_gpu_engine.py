@@ -468,13 +468,16 @@ def test_wide_decode_batch_vs_oracle(tmp_path):
     np.testing.assert_allclose(blob, state_to_blob(state)[[0, 17, 39]], rtol=1e-4, atol=1e-4)
 
 
-def test_c4_shape_64_streams_32_steps_vs_oracle(tmp_path):
+@pytest.mark.parametrize("layer", ["0", "1"])
+def test_c4_shape_64_streams_32_steps_vs_oracle(tmp_path, monkeypatch, layer):
     """The production decode shape of C4: 64 streams of the 0.1B model (four
     full 16-row tiles of every decode product, the M = 64 wide LM head, the
     K-split FFN output and the fused ROSA-out), a short prompt, then 32
     teacher-forced decode steps replayed from the step graph, against the
     float64 oracle: logits within 1e-3 at every step, identical greedy ids
-    wherever the top-2 gap exceeds 1e-3, carried states within 1e-4."""
+    wherever the top-2 gap exceeds 1e-3, carried states within 1e-4.  Layer
+    "1" runs the same steps through the persistent decode layers."""
+    monkeypatch.setenv("YUF_DECODE_LAYER", layer)
     cfg = PRESETS["0.1b"]
     weights = synth_weights(cfg, seed=21)
     path = tmp_path / "m.yuf"
@@ -631,19 +634,23 @@ def test_device_sampling_ties():
     assert len(seen0) > 8  # the 32 tied logits are drawn uniformly
 
 
-@pytest.mark.parametrize("preset,branches", [("tiny", 1), ("tiny", 2), ("tiny", 3), ("0.1b", 2), ("0.1b", 4)])
-def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, preset, branches):
+@pytest.mark.parametrize("preset,branches,layer", [("tiny", 1, "0"), ("tiny", 2, "0"), ("tiny", 3, "0"),
+                                                  ("0.1b", 2, "0"), ("0.1b", 4, "0"), ("0.1b", 1, "1")])
+def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, preset, branches, layer):
     """Decode steps replayed from the captured HIP graph equal eager steps
     bit for bit, across replays separated by other device work and host
     synchronisations, a change of batch size (re-capture) and the host-buffer
-    entry point.  The graph splits the streams into `branches` groups recorded
-    on forked HIP streams (uneven groups included); the eager engine runs the
-    whole batch as one pass.  The 0.1B shapes exercise the grouped decode
-    products and the SiLU-paired FFN slices at their real widths."""
+    entry point.  The per-kernel graph (layer "0") splits the streams into
+    `branches` groups recorded on forked HIP streams (uneven groups
+    included); the eager engine runs the whole batch as one pass.  The 0.1B
+    shapes exercise the grouped decode products and the SiLU-paired FFN
+    slices at their real widths; layer "1" replays the persistent decode
+    layers (their counters zeroed by a fill node of the graph)."""
     cfg = PRESETS[preset]
     path = tmp_path / "tiny.yuf"
     write_yuf(path, cfg, synth_weights(cfg, seed=3))
     ck = Checkpoint.load(path)
+    monkeypatch.setenv("YUF_DECODE_LAYER", layer)
     monkeypatch.setenv("YUF_DECODE_BRANCHES", str(branches))
     graph_eng = Engine(ck, max_streams=4, max_tokens=128)
     monkeypatch.setenv("YUF_NO_GRAPH", "1")
@@ -689,6 +696,7 @@ def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n
     prompt = uniform_tokens(12, n, 5, cfg.vocab_size)
     steps = uniform_tokens(13, n, 4, cfg.vocab_size)
     out = {}
+    monkeypatch.setenv("YUF_DECODE_LAYER", "0")  # the per-kernel decode path
     for fusion in ("1", "0"):
         monkeypatch.setenv("YUF_DECODE_FUSION", fusion)
         eng = Engine(ck, max_streams=n + 3, max_tokens=n * 5)
@@ -715,6 +723,7 @@ def test_tiled_decode_activations_are_bit_identical(tmp_path, monkeypatch, n):
     prompt = uniform_tokens(21, n, 5, cfg.vocab_size)
     steps = uniform_tokens(22, n, 3, cfg.vocab_size)
     out = {}
+    monkeypatch.setenv("YUF_DECODE_LAYER", "0")  # the per-kernel decode path
     for tiles in ("1", "0"):
         monkeypatch.setenv("YUF_DECODE_TILES", tiles)
         eng = Engine(ck, max_streams=n + 5, max_tokens=n * 5)
@@ -724,3 +733,37 @@ def test_tiled_decode_activations_are_bit_identical(tmp_path, monkeypatch, n):
         eng.close()
     np.testing.assert_array_equal(out["1"][0], out["0"][0])
     np.testing.assert_array_equal(out["1"][1], out["0"][1])
+
+
+@pytest.mark.parametrize("preset,n", [("0.1b", 64), ("0.1b", 40), ("0.1b", 5), ("0.1b", 1), ("d256_rosa256", 13)])
+def test_persistent_decode_layers_match_per_kernel_path(tmp_path, monkeypatch, preset, n):
+    """The persistent decode layers (YUF_DECODE_LAYER=1: one launch per layer;
+    streams split over the XCDs, stages joined by per-XCD barriers) against
+    the default per-kernel decode path on the same weights: logits within 1e-4 and every
+    carried state (previous, WKV, ROSA) within 1e-4 / 1e-5 over five steps,
+    with slots permuted so state rows are gathered and scattered through the
+    slot map; n = 5 and 1 leave most XCD groups empty, 40 fills them
+    unevenly; d256_rosa256 has head size 64 and ROSA 256.  Each path is held
+    to 1e-4 relative / 1e-5 absolute against the float64 oracle by the C4
+    tests, so two fp32 summation orders may differ by twice that: states are
+    compared at 2e-4 / 2e-5."""
+    print(f"persistent decode {preset} n={n}", flush=True)
+    cfg = PRESETS[preset] if preset in PRESETS else ModelConfig(
+        vocab_size=512, d_model=256, n_layers=2, n_heads=4, head_size=64, rosa_size=256)
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=23))
+    ck = Checkpoint.load(path)
+    slots = np.random.default_rng(n).permutation(n + 3)[:n].astype(np.int32)
+    prompt = uniform_tokens(31, n, 6, cfg.vocab_size)
+    steps = uniform_tokens(32, n, 5, cfg.vocab_size)
+    out = {}
+    for layer in ("1", "0"):
+        monkeypatch.setenv("YUF_DECODE_LAYER", layer)
+        eng = Engine(ck, max_streams=n + 3, max_tokens=n * 6)
+        eng.prefill(prompt, slots=slots, logits="none")
+        logits = [eng.step(steps[:, t], slots=slots) for t in range(steps.shape[1])]
+        out[layer] = (np.stack(logits), _states_from_blob(eng, slots))
+        eng.close()
+    assert np.isfinite(out["1"][0]).all()
+    np.testing.assert_allclose(out["1"][0], out["0"][0], rtol=0, atol=1e-4)
+    np.testing.assert_allclose(out["1"][1], out["0"][1], rtol=2e-4, atol=2e-5)

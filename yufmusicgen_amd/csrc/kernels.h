@@ -166,6 +166,51 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
 // Workspace the short-M path can use for an N-column product (floats).
 size_t gemm_workspace_floats(int N, int K);
 
+// --------------------------------------------------- persistent decode layer
+// One decode layer (T = 1) of up to kDlRows streams per XCD group in one
+// launch: the streams are split into `groups` groups (one per XCD), and the
+// workgroups running on XCD x (read from the hardware's XCC_ID) work through
+// group x's seven stages -- LN + token shift + r/k/v/w1/a1/g1 products; the
+// WKV step with the second low-rank stage; LN * g -> W_o (+h); LN -> ROSA
+// in; the ROSA step -> ROSA out (+h); LN -> FFN in (silu * gate); FFN out
+// (+h) -- taking work items from per-group queues and meeting at per-group
+// barriers (agent-scope counters; activations written by one workgroup are
+// read by another with L1-bypassing loads, which the XCD's shared L2 serves).
+constexpr int kDlRows = 8;
+constexpr int kDlMaxD = 640;
+constexpr int kDlStages = 7;
+constexpr int kDlCounterStride = 32;  // ints between counters (one per 128-byte line)
+// The launch takes `grid` workgroups, a multiple of `groups`: the workgroups
+// of an XCD split each stage's items by their rank blockIdx.x / groups.
+struct DecodeLayerParams {
+    int n = 0, groups = 0;
+    int d = 0, H = 0, N = 0, L = 0, D = 0;
+    const int *slot = nullptr;
+    const float *ln_t_w = nullptr, *ln_t_b = nullptr, *mix6 = nullptr;
+    // 16 x 16-tiled weights (GemmParams::Wt layout); K = d matrices have
+    // 16 d floats per row tile.
+    const float *wt_rkv[3] = {}, *wt_lr1[3] = {};  // r, k, v [d][d]; w1t, a1t, g1t [L][d]
+    const float *w2t = nullptr, *a2t = nullptr, *g2t = nullptr;  // row-major [d][L]
+    const float *w0 = nullptr, *a0 = nullptr, *k_k = nullptr, *k_a = nullptr;
+    const float *ln_o_w = nullptr, *ln_o_b = nullptr, *wt_o = nullptr;
+    const float *ln_r_w = nullptr, *ln_r_b = nullptr, *wt_rin = nullptr, *b_rin = nullptr;  // [3D][d], [3D]
+    const float *rosa_u = nullptr, *rosa_lam = nullptr, *wt_rout = nullptr;              // [d][D]
+    const float *ln_f_w = nullptr, *ln_f_b = nullptr, *wt_fin = nullptr;  // [8d][d], 64-row in/gate blocks
+    const float *wt_fout = nullptr;                                      // [d][4d]
+    // This layer's state slots and the step's activations.
+    float *prev = nullptr, *wkv = nullptr, *rosa = nullptr;
+    float *h = nullptr;       // [n][d]
+    float *buf = nullptr;     // groups x decode_layer_group_floats(d, L, D)
+    int *sync = nullptr;      // this launch's counters (decode_layer_sync_ints), zero at launch
+    int *error = nullptr;     // bit 1 set when a barrier wait gives up
+};
+bool decode_layer_ok(int d, int H, int N, int L, int D);
+size_t decode_layer_group_floats(int d, int L, int D);
+// Counter ints of one launch: the stage counters of every group and one
+// (XCD, rank) registration slot per workgroup of the `grid`.
+size_t decode_layer_sync_ints(int groups, int grid);
+hipError_t launch_decode_layer(const DecodeLayerParams &p, int grid, hipStream_t stream);
+
 // ---------------------------------------------------------------- elementwise
 hipError_t launch_embed(const int *tokens, int M, const float *table, int d, int vocab, float *out,
                         int *bad_token_flag, hipStream_t stream);
