@@ -15,8 +15,14 @@ In the same run:
   * the WKV-7 scan (C2: B=8, T=2048, H=16, N=40, zero state) timed with HIP
     events on the stream it runs on -> `roofline` (algorithmic bytes / time
     against the 8 TB/s HBM peak);
-  * the single-token WKV-7 step of C4 and the ROSA scan of a C3 layer ->
-    `decode_roofline`, `rosa_roofline` (HBM, the same way);
+  * `decode_roofline`: the whole C4 decode step's algorithmic bytes (646.5 MB:
+    weights, state read and written, logits) over its measured time, against
+    8 TB/s, with the operator-form single-token WKV-7 step kernel timed alone
+    beside it; the ROSA scan of a C3 layer -> `rosa_roofline`;
+  * `c5`: C5 as configured with bf16 weights -- the wide model (24 layers,
+    d_model 1024, 16 x 64 heads, ROSA 256), B = 32 x T = 8192 prefill in
+    T-chunks of 2048 (last-position logits), then 512 decode steps of the 32
+    streams with device top-k sampling (--no-c5 skips it);
   * the FFN in/gate projection GEMM of C3 (M=16384, N=5120, K=640) -> MFMA
     utilisation: fp32 products run as six bf16 MFMAs over three-part bf16
     splits, so the peak is the 2.5 PFLOP/s dense bf16 peak / 6 (416.7 TFLOP/s
@@ -28,10 +34,7 @@ In the same run:
 
 Only N = 1 GPU exists on these boxes; --gpus above 1 exits with a message.
 
-`--only c5` (not part of the default run): C5 as configured -- the wide model
-(24 layers, d_model 1024, 16 x 64 heads, ROSA 256) with bf16 projection weights,
-B = 32 x T = 8192 tokens of prefill (last-position logits), then 512 decode
-steps of the 32 streams -- and the same workload with fp32 weights.
+`--only c5`: the C5 leg alone, and the same workload with fp32 weights.
 
 `cpu_baseline_decode` / `cpu_baseline_scan`: the oracle's float32 single-token
 step of C4 (64 streams) and its sequential C2 scan, on the same host cores.
@@ -103,6 +106,38 @@ def bench_scan(iters: int) -> dict:
             "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
 
 
+def decode_step_bytes(cfg, streams: int) -> int:
+    """Algorithmic HBM bytes of one decode step (SURVEY-style count): every
+    weight once (the tied embedding once, as the LM head; the gathered rows are
+    negligible), each stream's recurrent state read and written (previous, WKV,
+    ROSA), and the V logits written.  0.1B model, 64 streams: 646.5 MB."""
+    from yufmusicgen_amd.synth import tensor_specs
+
+    params = sum(int(np.prod(shape)) for _, shape in tensor_specs(cfg))
+    state = cfg.n_layers * (cfg.d_model + cfg.n_heads * cfg.head_size ** 2 + cfg.rosa_size)
+    return 4 * (params + 2 * streams * state + streams * cfg.vocab_size)
+
+
+def decode_roofline(cfg, streams: int, ms_per_step: float, operator_leg: dict) -> dict:
+    """The whole decode step against the HBM roofline: algorithmic bytes per
+    step / measured step time (the step is a chain of dependent launches, so
+    this is the figure to move); beside it the operator-form WKV-7 step kernel
+    timed alone (wkv7_step_kernel<N,false,1,false> through yuf_wkv7_scan_f32,
+    not the in-model variant with the low-rank stage folded in, which only runs
+    inside the replayed step graph -- see profiles/decode_c4_kernel_stats.md)."""
+    nbytes = decode_step_bytes(cfg, streams)
+    achieved = nbytes / (ms_per_step * 1e-3) / 1e9
+    traffic = None
+    pmc = os.path.join(ROOT, "profiles", "decode_c4_traffic.json")
+    if os.path.exists(pmc):
+        with open(pmc) as handle:
+            traffic = json.load(handle).get("step", {}).get("traffic_bytes")
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": f"whole C4 decode step ({streams} streams, 0.1B model, graph-replayed)",
+            "algorithmic_bytes": nbytes, "ms_per_step": round(ms_per_step, 4), "wkv_step_operator": operator_leg}
+
+
 def bench_wkv_step(iters: int) -> dict:
     """The single-token WKV-7 step of C4 (64 streams, H=16, N=40, state read and
     written in place): 64 (2 H N^2 + 7 d) 4 bytes = 14.25 MB per layer-step."""
@@ -124,7 +159,8 @@ def bench_wkv_step(iters: int) -> dict:
     nbytes = B * (2 * H * N * N + 7 * H * N) * 4
     achieved = nbytes / (ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "kernel": "wkv7_step_kernel (C4: 64 streams, H=16, N=40, T=1)",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "kernel": "wkv7_step_kernel<40,false,1,false> operator form (C4: 64 streams, H=16, N=40, T=1)",
             "algorithmic_bytes": nbytes, "avg_us": round(ms * 1e3, 2)}
 
 
@@ -185,14 +221,14 @@ def bench_gemm(iters: int) -> dict:
             "avg_us": round(ms * 1e3, 1)}
 
 
-def bench_c5(args) -> dict:
+def bench_c5(args, weight_types=("bf16", "f32")) -> dict:
     """C5 as configured: the wide model (24 layers,
     d_model 1024, 16 x 64 heads, ROSA 256, V 20480) with bf16 projection weights
     and fp32 WKV / ROSA state; B = 32 rows x T = 8192 tokens of prefill
     (T-chunked through a 32 x 2048-token engine pass, the state carried,
     last-position logits), then 512 decode steps of the 32 streams with device
     top-k = 32, T = 1.0 sampling.  The fp32-weight engine runs the same workload
-    once for comparison."""
+    once for comparison (--only c5; the default run measures bf16 only)."""
     import torch
 
     from yufmusicgen_amd.checkpoint import write_yuf
@@ -215,6 +251,8 @@ def bench_c5(args) -> dict:
                        f"(T-chunks of {chunk}, last logits), then {D} decode steps of {B} streams "
                        "(device top-k=32 T=1.0 sampling)"}
     for wt, reps in (("bf16", max(1, args.c5_steps)), ("f32", 1)):
+        if wt not in weight_types:
+            continue
         engine = Engine(ckpt, max_streams=B, max_tokens=B * chunk, weight_dtype=wt)
         stream = torch.cuda.ExternalStream(engine.stream)
         logits = torch.empty(B, cfg.vocab_size, device="cuda")
@@ -342,8 +380,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--decode-steps", type=int, default=1024)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--c5-steps", type=int, default=2, help="timed C5 prefills (--only c5)")
-    ap.add_argument("--c5-decode-steps", type=int, default=512, help="C5 decode steps (--only c5)")
+    ap.add_argument("--c5-steps", type=int, default=2, help="timed C5 prefills")
+    ap.add_argument("--c5-decode-steps", type=int, default=512, help="C5 decode steps")
+    ap.add_argument("--no-c5", action="store_true", help="skip the C5 leg of the default run")
     ap.add_argument("--only", choices=["scan", "prefill", "decode", "copy", "c5", "kernels", "gemm"], default=None,
                     help="profiling aids: just the C2 scan (20 launches), just the prefill steps, just the C4 "
                          "decode leg, a plain 256 MiB device copy (20 launches) that calibrates the "
@@ -452,6 +491,12 @@ def main() -> int:
     engine.close()
     del logits
 
+    c5 = None
+    if not args.no_c5:
+        del engine
+        torch.cuda.empty_cache()
+        log("c5 (bf16 weights)")
+        c5 = bench_c5(args, weight_types=("bf16",))
     log("scan roofline")
     roofline = bench_scan(20)
     log(f"scan {roofline['avg_us']} us, {roofline['achieved']} GB/s")
@@ -496,12 +541,13 @@ def main() -> int:
         "decode_tokens_per_s": round(decode_tps, 1),
         "decode_ms_per_step": round(dec_elapsed * 1e3 / args.decode_steps, 3),
         "roofline": roofline,
-        "decode_roofline": step,
+        "decode_roofline": decode_roofline(cfg, S, dec_elapsed * 1e3 / args.decode_steps, step),
         "rosa_roofline": rosa,
         "gemm_roofline": gemm,
         "cpu_baseline": cpu,
         "cpu_baseline_decode": cpu_dec,
         "cpu_baseline_scan": cpu_scan,
+        "c5": c5,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -31,7 +31,7 @@ import torch
 from torch.nn import functional as F
 
 from .rosa import rosa_scan
-from .wkv7 import wkv7_scan
+from .wkv7 import wkv7_scan, wkv7_scan_chunked
 
 LN_EPS = 1e-5  # nn.LayerNorm default, model.py:89,346-356
 
@@ -55,11 +55,29 @@ def _bf16(x: torch.Tensor) -> torch.Tensor:
     return x.to(torch.float32).to(torch.bfloat16).to(x.dtype)
 
 
+def split16(x: torch.Tensor) -> torch.Tensor:
+    """An activation as the bf16-weight kernels multiply it: hi = bf16(x),
+    lo = bf16(x - hi), hi + lo (|x - (hi + lo)| <= 2^-16 |x|)."""
+    hi = _bf16(x)
+    return hi + _bf16(x - hi)
+
+
 class OracleModel:
-    def __init__(self, config: dict, weights: dict, dtype=torch.float64, bf16_linear: bool = False):
+    def __init__(self, config: dict, weights: dict, dtype=torch.float64, bf16_linear: bool = False,
+                 chunked_scan: bool = False, split_activations: bool = False):
         self.cfg = dict(config)
         self.dtype = dtype
         self.bf16_linear = bool(bf16_linear)
+        # chunked_scan: the WKV-7 scan in its 16-token chunk form
+        # (wkv7_scan_chunked, the same recurrence regrouped; pinned against the
+        # sequential loop in tests/test_oracle_wkv7.py) -- for long sequences,
+        # where the per-token loop dominates the oracle's time.
+        self.chunked_scan = bool(chunked_scan)
+        # split_activations: every projection multiplies split16(x) instead of
+        # x -- the engine's bf16-weight products, which split each fp32
+        # activation into two bf16 parts (a model of that engine, not of the
+        # reference, whose fp32 program multiplies x itself).
+        self.split_activations = bool(split_activations)
         self.d = int(self.cfg["d_model"])
         self.n_layers = int(self.cfg["n_layers"])
         self.heads = int(self.cfg["n_heads"])
@@ -95,6 +113,8 @@ class OracleModel:
 
     def _mm(self, x: torch.Tensor, m: torch.Tensor) -> torch.Tensor:
         """x @ m for a projection (m already in its product orientation)."""
+        if self.split_activations:
+            x = split16(x)
         return x @ m
 
     # ---------------------------------------------------------------- TimeMix
@@ -125,7 +145,8 @@ class OracleModel:
 
     def timemix(self, layer: int, x: torch.Tensor, state: LayerState):
         r, w, k, v, a, b, g = self.timemix_inputs(layer, x, state.previous)
-        y, memory = wkv7_scan(r, w, k, v, a, b, state.memory)
+        scan = wkv7_scan_chunked if self.chunked_scan and x.shape[1] > 1 else wkv7_scan
+        y, memory = scan(r, w, k, v, a, b, state.memory)
         y = y.reshape(x.shape)
         p = lambda s: self._p(layer, "time_mix." + s)  # noqa: E731
         z = F.layer_norm(y, (self.d,), p("out_norm.weight"), p("out_norm.bias"), LN_EPS)

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.model import OracleModel, blob_to_state, state_to_blob
+from oracle.model import LayerState, OracleModel, blob_to_state, state_to_blob
 from yufmusicgen_amd.checkpoint import write_yuf
 from yufmusicgen_amd.config import PRESETS, ModelConfig
 from yufmusicgen_amd.engine import Checkpoint, Engine, sample_device
@@ -541,9 +541,11 @@ def test_c4_as_configured_1024_steps_vs_oracle(tmp_path):
 
 
 def test_c5_bf16_24_layers_vs_fp32_oracle(tmp_path):
-    """C5 as configured: 24 layers, d = 1024, 16 x 64
-    heads, ROSA 256, V = 20480, bf16 projection weights (a version-2 .yuf) with
-    fp32 WKV / ROSA state, against the reference's fp32 program on the same
+    """The C5 architecture (24 layers, d = 1024,
+    16 x 64 heads, ROSA 256, V = 20480, bf16 projection weights from a
+    version-2 .yuf, fp32 WKV / ROSA state) at an oracle-sized batch -- 2 x 64
+    tokens in one pass, then two steps (the configured 32 x 8192 prefill and 512
+    steps: test_c5_as_configured_*) -- against the reference's fp32 program on the same
     bf16-valued weights -- every nn.Linear weight and the tied LM head, the
     embedding gather in f32 (model.py:406-431, evaluated in float64 by the oracle):
     logits within the configuration's 2e-2 at every position and step, and
@@ -767,3 +769,125 @@ def test_persistent_decode_layers_match_per_kernel_path(tmp_path, monkeypatch, p
     assert np.isfinite(out["1"][0]).all()
     np.testing.assert_allclose(out["1"][0], out["0"][0], rtol=0, atol=1e-4)
     np.testing.assert_allclose(out["1"][1], out["0"][1], rtol=2e-4, atol=2e-5)
+
+
+def _c5_check(got, ref, tol, what):
+    """Logits within tol and identical greedy ids where the reference's top-2
+    gap exceeds tol."""
+    np.testing.assert_allclose(got, ref, rtol=0, atol=tol, err_msg=what)
+    top2 = np.sort(ref, axis=-1)[..., -2:]
+    sure = top2[..., 1] - top2[..., 0] > tol
+    assert np.array_equal(np.argmax(got, -1)[sure], np.argmax(ref, -1)[sure]), what
+    return float(np.abs(got - ref).max())
+
+
+def test_c5_width_carried_chunks_vs_oracle(tmp_path):
+    """Two layers at C5's width (d = 1024, 16 x 64 heads, ROSA 256, bf16
+    weights): a 2 x 2048 prefill through an engine whose max_tokens forces two
+    carried T-chunks of 1024 (the N = 64 chunk scan and the D = 256 segmented
+    ROSA scan both continue from the carried state), then four decode steps,
+    against the float64 oracle on the stored bf16 weights: logits within C5's
+    2e-2 (and within 1e-3), greedy ids where the top-2 gap exceeds 2e-2.  The
+    carried states are held to the engine's own arithmetic: each bf16-weight
+    product multiplies a two-part bf16 split of the activation (2^-16
+    relative), so they are compared with the float64 oracle run on split
+    activations (split_activations=True), within three times the deviation
+    of that program in float32 from float64."""
+    cfg = ModelConfig(vocab_size=20480, d_model=1024, n_layers=2, n_heads=16, head_size=64, rosa_size=256)
+    path = tmp_path / "c5w.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=51), linear_bf16=True)
+    from yufmusicgen_amd.checkpoint import read_yuf
+
+    _, stored = read_yuf(path)
+    tokens = prompt_tokens(52, 2, 2048, cfg.vocab_size)
+    nxt = uniform_tokens(53, 2, 4, cfg.vocab_size)
+    eng = Engine(Checkpoint.load(path), max_streams=2, max_tokens=2 * 1024, weight_dtype="bf16")
+    got = [eng.prefill(tokens, logits="last")] + [eng.step(nxt[:, t]) for t in range(4)]
+    oracle = OracleModel(cfg.to_dict(), stored, bf16_linear=True, chunked_scan=True)
+    out, st = oracle.forward(tokens, logits="last")
+    ref = [out.numpy()]
+    for t in range(4):
+        out, st = oracle.step(nxt[:, t], st)
+        ref.append(out.numpy())
+    worst = max(_c5_check(g, r, 2e-2, f"output {i}") for i, (g, r) in enumerate(zip(got, ref)))
+    print(f"C5 width, two carried chunks: worst logit deviation {worst:.2e}", flush=True)
+    assert worst <= LOGIT_ATOL
+    split = {}
+    for dtype in (torch.float64, torch.float32):
+        model = OracleModel(cfg.to_dict(), stored, dtype=dtype, bf16_linear=True, chunked_scan=True,
+                            split_activations=True)
+        _, sst = model.forward(tokens, logits="none")
+        for t in range(4):
+            _, sst = model.step(nxt[:, t], sst)
+        split[dtype] = state_to_blob(sst)
+    ref_blob, st32 = split[torch.float64], split[torch.float32]
+    print(f"split activations move the float64 states by {float(np.abs(ref_blob - state_to_blob(st)).max()):.2e}",
+          flush=True)
+    fp32_dev = float(np.abs(st32 - ref_blob).max())
+    got_dev = float(np.abs(_states_from_blob(eng, range(2)) - ref_blob).max())
+    print(f"states: engine {got_dev:.2e}, float32 program {fp32_dev:.2e} from float64", flush=True)
+    assert got_dev <= 3.0 * fp32_dev + 1e-5, (got_dev, fp32_dev)
+
+
+def test_c5_as_configured_32x8192_then_512_steps(tmp_path):
+    """C5 at its configured size: the 24-layer bf16
+    wide model prefills B = 32 x T = 8192 through 32 x 2048-token T-chunks
+    (the state carried between them), against the same prefill in chunks of
+    1024 (last logits within 1e-4; every carried state within 2e-3: the two
+    chunkings are two fp32 evaluation orders of one program -- at a chunk
+    boundary the next ROSA segment starts from a 64-token sequential scan
+    where the other composes A^64 -- and after 24 layers and 8192 tokens
+    their states drift apart by up to ~7e-4 while the last logits stay
+    within 1e-4; carrying itself is pinned against the oracle by
+    test_c5_width_carried_chunks_vs_oracle); sequence
+    5 followed over all 8192 tokens by the float64 oracle on the stored bf16
+    weights (logits within 2e-2, greedy ids where the top-2 gap exceeds 2e-2);
+    then 512 decode steps of all 32 streams (finite logits throughout), with
+    streams 5 (the oracle's own state) and 17 (starting from the engine's
+    saved state) followed by the oracle for the first 32 steps at 2e-2."""
+    cfg = PRESETS["wide"]
+    path = tmp_path / "c5.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=41), linear_bf16=True)
+    from yufmusicgen_amd.checkpoint import read_yuf
+
+    _, stored = read_yuf(path)
+    B, T, steps, follow = 32, 8192, 512, 32
+    tokens = prompt_tokens(42, B, T, cfg.vocab_size)
+    ck = Checkpoint.load(path)
+    print("C5: prefill in T-chunks of 1024", flush=True)
+    eng = Engine(ck, max_streams=B, max_tokens=B * 1024, weight_dtype="bf16")
+    last_1k = eng.prefill(tokens, logits="last")
+    states_1k = _states_from_blob(eng, range(B))
+    eng.close()
+    del eng
+    torch.cuda.empty_cache()
+    print("C5: prefill in T-chunks of 2048", flush=True)
+    eng = Engine(ck, max_streams=B, max_tokens=B * 2048, weight_dtype="bf16")
+    last = eng.prefill(tokens, logits="last")
+    states = _states_from_blob(eng, range(B))
+    assert np.isfinite(last).all()
+    np.testing.assert_allclose(last, last_1k, rtol=0, atol=1e-4)
+    sdev = np.abs(states - states_1k)
+    print(f"C5 chunkings: last logits {float(np.abs(last - last_1k).max()):.2e} apart, states "
+          f"{float(sdev.max()):.2e} apart ({float(np.mean(sdev > 1e-4)):.2%} beyond 1e-4)", flush=True)
+    np.testing.assert_allclose(states, states_1k, rtol=0, atol=2e-3)
+    del states_1k, sdev
+    print("C5: float64 oracle over sequence 5 (8192 tokens)", flush=True)
+    oracle = OracleModel(cfg.to_dict(), stored, bf16_linear=True, chunked_scan=True)
+    ref, st5 = oracle.forward(tokens[5:6], logits="last")
+    dev = _c5_check(last[5:6], ref.numpy(), 2e-2, "prefill logits, sequence 5")
+    sdev = float(np.abs(states[5:6] - state_to_blob(st5)).max())
+    print(f"C5 prefill, sequence 5: logits {dev:.2e} and states {sdev:.2e} from the float64 oracle", flush=True)
+    st17 = blob_to_state(states[17:18], cfg.to_dict())
+    ost = [LayerState(torch.cat((a.previous, b.previous)), torch.cat((a.memory, b.memory)),
+                      torch.cat((a.rosa, b.rosa))) for a, b in zip(st5, st17)]
+    nxt = uniform_tokens(43, B, steps, cfg.vocab_size)
+    worst = 0.0
+    for t in range(steps):
+        g = eng.step(nxt[:, t])
+        assert np.isfinite(g).all(), f"step {t}"
+        if t < follow:
+            r, ost = oracle.step(nxt[[5, 17], t], ost)
+            worst = max(worst, _c5_check(g[[5, 17]], r.numpy(), 2e-2, f"step {t}"))
+    print(f"C5 decode, streams 5 and 17 over {follow} steps: worst deviation {worst:.2e}; {steps} steps run",
+          flush=True)

@@ -134,3 +134,23 @@ def test_bf16_oracle_rounds_projection_operands_only():
     rounded = OracleModel(cfg.to_dict(), {n: v.numpy() for n, v in model.w.items()})  # incl. the rounded head
     c, _ = rounded.forward(ids)
     assert torch.equal(a, c)
+
+
+def test_split16_is_the_two_part_bf16_split():
+    """split16(x) = hi + lo with hi = bf16(x), lo = bf16(x - hi): within 2^-16
+    relative of x, both parts exact bf16 values, and x itself when x is a
+    bf16 value (lo = 0)."""
+    import torch
+
+    from oracle.model import split16
+
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(20000, generator=g, dtype=torch.float64) * torch.exp(torch.randn(20000, generator=g))).to(torch.float32).double()
+    s = split16(x)
+    assert torch.all((s - x).abs() <= 2.0 ** -16 * x.abs())
+    hi = x.float().bfloat16().double()
+    lo = s - hi
+    assert torch.equal(lo, lo.float().bfloat16().double())
+    assert torch.equal(split16(hi), hi)
+    # A plain bf16 rounding (one part) misses the same bound.
+    assert torch.any((hi - x).abs() > 2.0 ** -16 * x.abs())
