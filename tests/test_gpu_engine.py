@@ -680,19 +680,32 @@ def test_decode_graph_replays_match_eager(golden_dir, tmp_path, monkeypatch, pre
         np.testing.assert_array_equal(graph_eng.step(ids), eager_eng.step(ids))
 
 
-@pytest.mark.parametrize("preset,n", [("0.1b", 40), ("0.1b", 64), ("d256_rosa256", 5)])
-def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n):
+@pytest.mark.parametrize("preset,n,wdtype", [("0.1b", 40, "f32"), ("0.1b", 64, "f32"), ("d256_rosa256", 5, "f32"),
+                                            ("d512", 21, "bf16"), ("c5_width", 32, "bf16")])
+def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n, wdtype):
     """The folded decode kernels (second low-rank stage inside the WKV step,
     ROSA step as the ROSA-out prologue with the tile's last workgroup writing
-    the memory) against the separate kernels (YUF_DECODE_FUSION=0): logits and
-    every carried state over several steps, with slots permuted so the ROSA
-    rows are gathered and scattered through the slot map."""
+    the memory, FFN output split over K) against the separate kernels
+    (YUF_DECODE_FUSION=0): logits and every carried state over several
+    steps, with slots permuted so the ROSA rows are gathered and scattered
+    through the slot map.  bf16 weights: the folds read the bf16-valued fp32
+    copy of their weights and multiply fp32 activations, where the separate
+    bf16 products multiply the two-part bf16 split of the activations
+    (2^-16 relative); d512 (8 x 64 heads, ROSA 128) takes the 16 x 16-tiled
+    decode activations with bf16 weights, c5_width is C5's layer shape
+    (d 1024, 16 x 64, ROSA 256) with C5's 32 streams."""
     # d256_rosa256: head size 64 and ROSA 256 (two 16-k steps per wave) on a small model.
-    cfg = PRESETS[preset] if preset in PRESETS else ModelConfig(
-        vocab_size=512, d_model=256, n_layers=2, n_heads=4, head_size=64, rosa_size=256)
+    if preset in PRESETS:
+        cfg = PRESETS[preset]
+    elif preset == "c5_width":
+        cfg = ModelConfig(vocab_size=20480, d_model=1024, n_layers=2, n_heads=16, head_size=64, rosa_size=256)
+    elif preset == "d512":
+        cfg = ModelConfig(vocab_size=512, d_model=512, n_layers=2, n_heads=8, head_size=64, rosa_size=128)
+    else:
+        cfg = ModelConfig(vocab_size=512, d_model=256, n_layers=2, n_heads=4, head_size=64, rosa_size=256)
     weights = synth_weights(cfg, seed=11)
     path = tmp_path / "m.yuf"
-    write_yuf(path, cfg, weights)
+    write_yuf(path, cfg, weights, linear_bf16=wdtype == "bf16")
     ck = Checkpoint.load(path)
     slots = np.random.default_rng(5).permutation(n + 3)[:n].astype(np.int32)
     prompt = uniform_tokens(12, n, 5, cfg.vocab_size)
@@ -701,13 +714,15 @@ def test_decode_fusion_matches_separate_kernels(tmp_path, monkeypatch, preset, n
     monkeypatch.setenv("YUF_DECODE_LAYER", "0")  # the per-kernel decode path
     for fusion in ("1", "0"):
         monkeypatch.setenv("YUF_DECODE_FUSION", fusion)
-        eng = Engine(ck, max_streams=n + 3, max_tokens=n * 5)
+        eng = Engine(ck, max_streams=n + 3, max_tokens=n * 5, weight_dtype=wdtype)
         eng.prefill(prompt, slots=slots, logits="none")
         logits = [eng.step(steps[:, t], slots=slots) for t in range(steps.shape[1])]
         out[fusion] = (np.stack(logits), _states_from_blob(eng, slots))
         eng.close()
+    # bf16: the two paths' activations differ by the 2^-16 split (above).
+    atol_state = 1e-5 if wdtype == "f32" else 1e-4
     np.testing.assert_allclose(out["1"][0], out["0"][0], rtol=0, atol=1e-4)
-    np.testing.assert_allclose(out["1"][1], out["0"][1], rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(out["1"][1], out["0"][1], rtol=1e-4, atol=atol_state)
 
 
 @pytest.mark.parametrize("n", [40, 64])

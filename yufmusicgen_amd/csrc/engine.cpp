@@ -162,16 +162,36 @@ int hip_fail(hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail(e_, what);     \
     } while (0)
 
-// Host-side weight preparation: the device layout the kernels want.
-int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<size_t> &offsets, std::string &err) {
+// x rounded to the nearest bf16 value (ties to even; NaN stays NaN), as float.
+float bf16_round(float x) {
+    uint32_t u;
+    std::memcpy(&u, &x, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return x;
+    u = ((u + 0x7fffu + ((u >> 16) & 1u)) >> 16) << 16;
+    std::memcpy(&x, &u, 4);
+    return x;
+}
+
+// Host-side weight preparation: the device layout the kernels want.  With
+// round_projections (bf16 weights) every projection matrix -- the nn.Linear
+// weights, the low-rank pairs and the LM head -- is stored as its bf16 value,
+// so kernels that read the fp32 copy (the decode folds) multiply exactly the
+// weights the bf16 products use.
+int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<size_t> &offsets, std::string &err,
+                  bool round_projections = false) {
     const ModelShape &s = ck.shape;
     const long long d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4LL * s.d;
+    std::vector<std::pair<size_t, size_t>> projections;  // (offset, count) of each projection matrix
     auto append = [&](const float *src, size_t n) {
         // Keep every tensor 256-byte aligned for vector loads.
         size_t off = (host.size() + 63) & ~size_t(63);
         host.resize(off + n);
         std::memcpy(host.data() + off, src, n * sizeof(float));
         offsets.push_back(off);
+    };
+    auto append_proj = [&](const float *src, size_t n) {
+        append(src, n);
+        projections.emplace_back(offsets.back(), n);
     };
     auto get = [&](const std::string &name, std::vector<long long> dims) -> const float * {
         return ck.tensor(name, dims, err);
@@ -190,7 +210,7 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
         head = get("lm_head.weight", {V, d});
         if (!head) return YUF_ERR_FORMAT;
     }
-    append(head, (size_t)(V * d));
+    append_proj(head, (size_t)(V * d));
     for (const char *n : {"final_norm.weight", "final_norm.bias"}) {
         const float *p = get(n, {d});
         if (!p) return YUF_ERR_FORMAT;
@@ -207,14 +227,14 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
         auto mat = [&](const std::string &n, long long rows, long long cols) -> bool {
             const float *p = get(pre + n, {rows, cols});
             if (!p) return false;
-            append(p, (size_t)(rows * cols));
+            append_proj(p, (size_t)(rows * cols));
             return true;
         };
         auto mat_t = [&](const std::string &n, long long rows, long long cols) -> bool {
             const float *p = get(pre + n, {rows, cols});
             if (!p) return false;
             std::vector<float> t = transposed(p, rows, cols);
-            append(t.data(), t.size());
+            append_proj(t.data(), t.size());
             return true;
         };
         if (!vec("norm_time.weight") || !vec("norm_time.bias")) return YUF_ERR_FORMAT;
@@ -249,7 +269,7 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
                 std::memcpy(w3.data() + c * D * d, w, (size_t)(D * d) * sizeof(float));
                 std::memcpy(b3.data() + c * D, b, (size_t)D * sizeof(float));
             }
-            append(w3.data(), w3.size());
+            append_proj(w3.data(), w3.size());
             append(b3.data(), b3.size());
         }
         if (!vec("rosa.householder") || !vec("rosa.decay") || !mat("rosa.output.weight", d, D)) return YUF_ERR_FORMAT;
@@ -268,7 +288,7 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
                 std::memcpy(cat.data() + (size_t)(q * 64) * d, wi + (size_t)(q * 32) * d, 32 * d * sizeof(float));
                 std::memcpy(cat.data() + (size_t)(q * 64 + 32) * d, wg + (size_t)(q * 32) * d, 32 * d * sizeof(float));
             }
-            append(cat.data(), cat.size());
+            append_proj(cat.data(), cat.size());
         }
         if (!mat("ffn_out.weight", d, hid)) return YUF_ERR_FORMAT;
         {
@@ -308,6 +328,9 @@ int build_weights(const Checkpoint &ck, std::vector<float> &host, std::vector<si
             append(lf.data(), lf.size());
         }
     }
+    if (round_projections)
+        for (const auto &[off, n] : projections)
+            for (size_t i = 0; i < n; ++i) host[off + i] = bf16_round(host[off + i]);
     return YUF_OK;
 }
 
@@ -464,7 +487,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     // Decode: the FFN output product is split over K into kFfnParts products
     // (four times the workgroups); the partial sums stay in a.kpart until the
     // next layer's ln_shift (or, after the last layer, add_parts) adds them to h.
-    const bool ffn_split = Tc == 1 && e.decode_fusion && !e.w_h && M <= 64 && d <= 1024 &&
+    const bool ffn_split = Tc == 1 && e.decode_fusion && M <= 64 && d <= 1024 &&
                            hid % (16 * kFfnParts) == 0 && !decode_layer_applies(e, n);
     // Decode activations that only feed the decode GEMMs (the token-shift mixes,
     // the WKV output and gate, the FFN hidden rows) are written in 16 x 16 tiles
@@ -473,8 +496,11 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
     // per wave (d <= 768) and room for whole 16-row tiles.
     // With several stream groups (parallel graph branches) a group's tiles must
     // not cover another group's rows: whole tiles only.
+    // (d <= 768 with fp32 weights, 16-k steps; d <= 512 with bf16 weights,
+    // 32-k steps: W_o's gated LN prologue and the SiLU-pair FFN input hold at
+    // most 6 and 2 steps per wave in registers.)
     const bool tl = ffn_split && e.act_tiles && a.tile_aligned && (!a.grouped || M % 16 == 0) && d % 16 == 0 &&
-                    d <= 768 && wkv7_step_lowrank_ok(s.head_size, L) && ((M + 15) / 16) * 16 <= e.max_tokens;
+                    d <= (e.w_h ? 512 : 768) && wkv7_step_lowrank_ok(s.head_size, L) && ((M + 15) / 16) * 16 <= e.max_tokens;
     if (Tc == 1 && decode_layer_applies(e, n)) {
         // One launch per layer; its counters start at zero (a fill kernel, not
         // a memset node, so the step can be captured and replayed).
@@ -546,8 +572,9 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         const float *mr = a.mix, *mw = a.mix + plane, *mk = a.mix + 2 * plane, *mv = a.mix + 3 * plane,
                     *ma = a.mix + 4 * plane, *mg = a.mix + 5 * plane;
         int rc;
-        // Decode with fp32 weights: the second low-rank stage runs inside the WKV step.
-        const bool fuse_lr = Tc == 1 && e.decode_fusion && !e.w_h && wkv7_step_lowrank_ok(s.head_size, L);
+        // Decode: the second low-rank stage runs inside the WKV step (which reads
+        // the fp32 copy of w2t / a2t / g2t; bf16-valued in bf16 mode).
+        const bool fuse_lr = Tc == 1 && e.decode_fusion && wkv7_step_lowrank_ok(s.head_size, L);
         {
             // r, k, v and the three low-rank first stages (one launch for short
             // products, two otherwise: the tile widths differ); then the second stages.
@@ -591,7 +618,7 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
         if ((rc = ln_gemm(e, st, M, 3 * D, d, a.h, d, w.ln_r_w, w.ln_r_b, nullptr, a.xn, w.rosa_w3, a.rosa3, 3 * D,
                           w.rosa_b3)) != YUF_OK)
             return rc;
-        if (Tc == 1 && e.decode_fusion && !e.w_h && rosa_out_decode_ok(M, D)) {
+        if (Tc == 1 && e.decode_fusion && rosa_out_decode_ok(M, D)) {
             // Decode: the ROSA step runs as the A prologue of the ROSA-out product.
             RosaOutParams ro;
             ro.M = M; ro.N = d; ro.D = D;
@@ -970,7 +997,7 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
     std::vector<size_t> offs;
     std::string err;
     try {
-        int rc = build_weights(ck, host, offs, err);
+        int rc = build_weights(ck, host, offs, err, weight_type == YUF_WEIGHTS_BF16);
         if (rc != YUF_OK) return fail(rc, err);
     } catch (const std::bad_alloc &) {
         return fail(YUF_ERR_OOM, "out of host memory preparing weights");
