@@ -128,6 +128,29 @@ int yuf_linear_f32(int M, int N, int K, const float *A, const float *W, const fl
                    const float *residual, float *C, void *stream);
 
 /*
+ * Pre-split weights for yuf_linear_f32 (no counterpart in the reference: a
+ * one-time preparation of an nn.Linear weight, as the engine does for every
+ * projection matrix at creation).  The large-tile products (M > 64, K % 32
+ * == 0) run fp32 as six bf16 matrix-core products over three-part splits of
+ * A and W; yuf_x3_split_planes stores W's three parts once, in the layout the
+ * kernel streams into LDS directly, so products that pass them skip W's
+ * split and stage both operands by direct memory -> LDS loads.
+ *   yuf_x3_planes_elems: uint16 elements of the planes of an [N, K] W, 0
+ *     unless N % 16 == 0 and K % 32 == 0.
+ *   yuf_x3_split_planes: W [N, K] fp32 (16-byte aligned) -> planes (16-byte
+ *     aligned device buffer of yuf_x3_planes_elems(N, K) elements), on
+ *     `stream`.
+ *   yuf_linear_f32_planes: yuf_linear_f32 with W's planes as well as W; the
+ *     results are bit-identical to yuf_linear_f32's (the planes are used where
+ *     the large-tile X3 path runs and A's rows are 16-byte aligned, W
+ *     elsewhere).
+ */
+size_t yuf_x3_planes_elems(int N, int K);
+int yuf_x3_split_planes(int N, int K, const float *W, uint16_t *planes, void *stream);
+int yuf_linear_f32_planes(int M, int N, int K, const float *A, const float *W, const uint16_t *Wp,
+                          const float *bias, int act, const float *residual, float *C, void *stream);
+
+/*
  * LayerNorm -> (gate) -> Linear in one kernel, for short products (M <= 64, the
  * decode shapes): C = (LayerNorm(A) * gamma + beta) [* gate] W^T + bias + residual.
  * The norm -> projection pairs of a block: out_norm(y) * g -> output

@@ -411,6 +411,34 @@ def test_prefill_stream_groups_are_bit_identical(tmp_path, monkeypatch, preset, 
             np.testing.assert_array_equal(a, b)
 
 
+@pytest.mark.parametrize("preset,n,T,logits", [
+    ("0.1b", 4, 256, "all"),    # every prefill product at 1024 rows, the LM head over all positions
+    ("0.1b", 3, 300, "last"),   # 900 rows: row tails of the 256-row tiles
+    ("wide2", 2, 256, "all"),   # d = 1024: FFN 8192 wide, ROSA 256
+])
+def test_prefill_with_weight_planes_is_bit_identical(tmp_path, monkeypatch, preset, n, T, logits):
+    """The engine's pre-split weight planes (the large-tile X3 products stream
+    W's three bf16 parts into LDS by direct loads, YUF_GEMM_PLANES unset)
+    against an engine created with YUF_GEMM_PLANES=0 (the kernel splits W as
+    it stages it): logits, states and a following decode step bit for bit."""
+    import dataclasses
+    cfg = dataclasses.replace(PRESETS["wide"], n_layers=2) if preset == "wide2" else PRESETS[preset]
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=21))
+    ck = Checkpoint.load(path)
+    tokens = uniform_tokens(22, n, T, cfg.vocab_size)
+    outs = []
+    for planes in ("1", "0"):
+        monkeypatch.setenv("YUF_GEMM_PLANES", planes)
+        eng = Engine(ck, max_streams=n, max_tokens=n * T)
+        got = eng.prefill(tokens, logits=logits)
+        nxt = eng.step(tokens[:, 0])
+        outs.append((got, nxt, _states_from_blob(eng, list(range(n)))))
+        eng.close()
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)
+
+
 def test_prefill_parts_and_decode_groups_interleaved(tmp_path, monkeypatch):
     """Prefills in parts and graph-replayed decode steps in two stream groups
     share the engine's side streams and fork / join events: alternate them

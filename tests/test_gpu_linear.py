@@ -123,3 +123,89 @@ def test_large_tile_products_hold_fp32_accuracy(m, n, k):
     assert np.all(err <= (k + 3) * 2.0 ** -24 * mag), float((err / mag).max())
     # Typical error stays at fp32's level (relative to the magnitude sum).
     assert float(np.median(err / mag)) < 4 * 2.0 ** -24
+
+
+@pytest.mark.parametrize("m,n,k,extras", [
+    (256, 5120, 640, "none"), (300, 5120, 640, "bias_tanh"), (4096, 5120, 640, "none"),   # 256-wide tiles
+    (1000, 640, 2560, "residual"), (2048, 640, 640, "bias_sigmoid"),                      # 160-wide tiles
+    (700, 384, 640, "alias"), (512, 128, 64, "none"),                                     # 128-wide tiles
+    (300, 192, 640, "bias"), (257, 64, 32, "none"),                                       # 64-wide tiles
+    (1000, 48, 64, "none"),   # no large-tile width fits: the planes are not used
+    (64, 640, 640, "none"),   # decode path: the planes are not used
+    (999, 640, 640, "offset"),   # A rows not 16-byte aligned: W is split by the kernel as before
+])
+def test_linear_with_weight_planes_is_bit_identical(m, n, k, extras):
+    """The pre-split-plane X3 kernel (yuf_linear_f32_planes, W's three bf16
+    parts prepared once by yuf_x3_split_planes and streamed into LDS with
+    direct loads) against yuf_linear_f32, whose large-tile kernel splits W
+    itself: the same splits and product order, so every output must be
+    bit-identical, on every tile width, row tail, epilogue (bias, tanh /
+    sigmoid, residual, residual aliasing C) and on the shapes where the planes
+    are bypassed.  Also checks that the planes path is actually taken where it
+    applies (the kernel trace is not visible here, so the check is that a
+    corrupted plane buffer changes the result exactly there)."""
+    print(f"linear planes {m}x{n}x{k} {extras}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(m * 7 + n + k)
+    off = 1 if extras == "offset" else 0
+    a_store = torch.randn(m * k + off, generator=g).cuda()
+    a = a_store[off:].view(m, k)
+    w = (torch.randn(n, k, generator=g) * 0.05).cuda()
+    bias = (torch.randn(n, generator=g) * 0.1).cuda() if "bias" in extras else None
+    act = 1 if "tanh" in extras else 2 if "sigmoid" in extras else 0
+    res = torch.randn(m, n, generator=g).cuda() if extras in ("residual", "alias") else None
+    st = torch.cuda.current_stream().cuda_stream
+    elems = lib().yuf_x3_planes_elems(n, k)
+    assert elems == n * k * 3
+    planes = torch.empty(elems, dtype=torch.int16, device="cuda")
+    check(lib().yuf_x3_split_planes(n, k, w.data_ptr(), planes.data_ptr(), st))
+
+    def run(use_planes, wp=None):
+        c = res.clone() if extras == "alias" else torch.full((m, n), float("nan"), device="cuda")
+        r = c if extras == "alias" else res
+        args = (a.data_ptr(), w.data_ptr())
+        tail = (None if bias is None else bias.data_ptr(), act, None if r is None else r.data_ptr(), c.data_ptr(), st)
+        if use_planes:
+            check(lib().yuf_linear_f32_planes(m, n, k, *args, (planes if wp is None else wp).data_ptr(), *tail))
+        else:
+            check(lib().yuf_linear_f32(m, n, k, *args, *tail))
+        torch.cuda.synchronize()
+        return c
+
+    ref, got = run(False), run(True)
+    assert not torch.isnan(ref).any()
+    assert torch.equal(ref, got), f"max diff {float((ref - got).abs().max())}"
+    # Zeroed planes change the result exactly where the planes path runs.
+    applies = m > 64 and n % 64 == 0 and k % 32 == 0 and extras != "offset"
+    zeroed = run(True, torch.zeros_like(planes))
+    assert torch.equal(zeroed, ref) != applies
+
+
+def test_weight_planes_layout():
+    """yuf_x3_split_planes against the layout written out on the host: part p
+    of W[n, k] (x1 = bf16(w), x2 = bf16(w - x1), x3 = bf16(w - x1 - x2), each
+    rounded to nearest even) at element ((n // 16 * (K // 32) + k // 32) * 3 +
+    p) * 512 + (n % 16) * 32 + 8 * ((k % 32 // 8) ^ s(n % 16)) + k % 8, with
+    s(r) = ((r >> 1) ^ (r >> 3)) & 3; and the parts sum back to w within
+    2^-24 relative."""
+    n, k = 48, 96
+    g = torch.Generator(device="cpu").manual_seed(5)
+    w = torch.randn(n, k, generator=g)
+    planes = torch.empty(lib().yuf_x3_planes_elems(n, k), dtype=torch.int16, device="cuda")
+    check(lib().yuf_x3_split_planes(n, k, w.cuda().data_ptr(), planes.data_ptr(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    got = planes.cpu().view(torch.bfloat16).float()
+    x1 = w.to(torch.bfloat16).float()
+    x2 = (w - x1).to(torch.bfloat16).float()
+    x3 = (w - x1 - x2).to(torch.bfloat16).float()
+    parts = [x1, x2, x3]
+    want = torch.empty_like(got)
+    for row in range(n):
+        for col in range(k):
+            r = row % 16
+            s = ((r >> 1) ^ (r >> 3)) & 3
+            for p in range(3):
+                o = ((row // 16 * (k // 32) + col // 32) * 3 + p) * 512 + r * 32 + 8 * (((col % 32) // 8) ^ s) + col % 8
+                want[o] = parts[p][row, col]
+    assert torch.equal(got, want)
+    err = (x1.double() + x2.double() + x3.double() - w.double()).abs()
+    assert bool((err <= 2.0 ** -24 * w.double().abs()).all())

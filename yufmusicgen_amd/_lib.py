@@ -48,6 +48,9 @@ SIGNATURES = {
     "yuf_rosa_scan_f32_noalloc": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_ln_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
+    "yuf_x3_planes_elems": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "yuf_x3_split_planes": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p]),
+    "yuf_linear_f32_planes": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 4 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_linear_bf16w": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_ln_linear_bf16w": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_ckpt_load": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(c_void_p)]),

@@ -18,6 +18,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <memory>
@@ -63,7 +64,7 @@ struct Engine {
     ModelShape s;
     int max_streams = 0, max_tokens = 0;
     hipStream_t stream = nullptr;
-    DeviceBuf weights, weights_h, weights_t, state, work, io, dl;
+    DeviceBuf weights, weights_h, weights_t, weights_p, state, work, io, dl;
     // bf16 mode: a bf16 image of the weight buffer (same element offsets); the
     // GEMMs of weights inside [w_base, w_base + w_floats) read it instead.
     const float *w_base = nullptr;
@@ -77,6 +78,9 @@ struct Engine {
         long long rows, cols;
         const void *tiles;
         int wt_ld;  // elements per row tile
+        // fp32 mode: the matrix's three bf16 parts for the large-tile X3
+        // products (GemmParams::Wp), or nullptr.
+        const uint16_t *planes;
     };
     std::vector<Tiled> tiled;
     std::vector<LayerW> layers;
@@ -356,6 +360,18 @@ const void *tiled_copy(const Engine &e, const float *W, int ldw, int *wt_ld) {
     return nullptr;
 }
 
+// The pre-split planes of W (rows r0 .. r0 + N of one of e.tiled's matrices,
+// all of its columns, r0 % 16 == 0) for the large-tile X3 products, or nullptr.
+const uint16_t *planes_copy(const Engine &e, const float *W, int ldw, int N, int K) {
+    for (const Engine::Tiled &t : e.tiled) {
+        if (!t.planes || W < t.base || W >= t.base + t.rows * t.cols || ldw != t.cols || K != t.cols) continue;
+        const long long off = W - t.base, r0 = off / t.cols, c0 = off % t.cols;
+        if (c0 != 0 || r0 % 16 != 0 || r0 + N > t.rows) return nullptr;
+        return t.planes + (size_t)(r0 / 16) * (t.cols / 32) * 3 * 512;
+    }
+    return nullptr;
+}
+
 GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, const float *W, int ldw, float *C,
                      int ldc, const float *bias = nullptr, int act = ACT_NONE, const float *residual = nullptr,
                      int ldr = 0, bool silu_pair = false) {
@@ -364,6 +380,7 @@ GemmParams make_gemm(Engine &e, int M, int N, int K, const float *A, int lda, co
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = ldr; p.silu_pair = silu_pair;
     p.workspace = e.gemm_ws; p.workspace_floats = e.gemm_ws_floats;
     if (e.w_h && W >= e.w_base && W < e.w_base + e.w_floats) p.Wh = e.w_h + (W - e.w_base);
+    if (!e.w_h && M > 64) p.Wp = planes_copy(e, W, ldw, N, K);
     if (M <= 64) {
         const void *t = tiled_copy(e, W, ldw, &p.wt_ld);
         if (e.w_h) p.Wht = static_cast<const uint16_t *>(t);
@@ -1052,15 +1069,15 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
         // Tiled copies of the decode products' matrices (from the host image).
         const long long d = s.d, L = s.low_rank, D = s.rosa, V = s.vocab, hid = 4LL * s.d;
         std::vector<Engine::Tiled> mats;
-        mats.push_back({e.head, V, d, nullptr, 0});
+        mats.push_back({e.head, V, d, nullptr, 0, nullptr});
         for (const LayerW &w : e.layers) {
-            for (const float *m : {w.w_r, w.w_k, w.w_v, w.w_o}) mats.push_back({m, d, d, nullptr, 0});
-            for (const float *m : {w.w1t, w.a1t, w.g1t}) mats.push_back({m, L, d, nullptr, 0});
-            for (const float *m : {w.w2t, w.a2t, w.g2t}) mats.push_back({m, d, L, nullptr, 0});
-            mats.push_back({w.rosa_w3, 3 * D, d, nullptr, 0});
-            mats.push_back({w.rosa_out, d, D, nullptr, 0});
-            mats.push_back({w.ffn_cat, 2 * hid, d, nullptr, 0});
-            mats.push_back({w.ffn_out, d, hid, nullptr, 0});
+            for (const float *m : {w.w_r, w.w_k, w.w_v, w.w_o}) mats.push_back({m, d, d, nullptr, 0, nullptr});
+            for (const float *m : {w.w1t, w.a1t, w.g1t}) mats.push_back({m, L, d, nullptr, 0, nullptr});
+            for (const float *m : {w.w2t, w.a2t, w.g2t}) mats.push_back({m, d, L, nullptr, 0, nullptr});
+            mats.push_back({w.rosa_w3, 3 * D, d, nullptr, 0, nullptr});
+            mats.push_back({w.rosa_out, d, D, nullptr, 0, nullptr});
+            mats.push_back({w.ffn_cat, 2 * hid, d, nullptr, 0, nullptr});
+            mats.push_back({w.ffn_out, d, hid, nullptr, 0, nullptr});
         }
         const bool bf16 = e.w_h != nullptr;
         const int kt = bf16 ? 32 : 16, esz = bf16 ? 2 : 4;
@@ -1096,6 +1113,30 @@ extern "C" int yuf_engine_create_ex(const yuf_ckpt *ckpt, int max_streams, int m
         for (size_t i = 0; i < mats.size(); ++i)
             mats[i].tiles = static_cast<const char *>(e.weights_t.p) + at[i] * esz;
         e.tiled = std::move(mats);
+        // fp32 mode: every projection matrix pre-split for the prefill's X3
+        // products (1.5 x the matrices' fp32 bytes; YUF_GEMM_PLANES=0 skips it).
+        const char *pe = std::getenv("YUF_GEMM_PLANES");
+        if (!bf16 && !(pe && std::strcmp(pe, "0") == 0)) {
+            size_t ptotal = 0;
+            std::vector<size_t> pat;
+            for (const Engine::Tiled &t : e.tiled) {
+                const size_t n = x3_planes_elems((int)t.rows, (int)t.cols);
+                pat.push_back(n ? ptotal : SIZE_MAX);
+                ptotal += ((n * 2 + 255) / 256) * 128;
+            }
+            if (ptotal) {
+                ENG_TRY(hipMalloc(&e.weights_p.p, ptotal * 2), "weight planes alloc");
+                uint16_t *pb = static_cast<uint16_t *>(e.weights_p.p);
+                for (size_t i = 0; i < e.tiled.size(); ++i) {
+                    Engine::Tiled &t = e.tiled[i];
+                    if (pat[i] == SIZE_MAX) continue;
+                    t.planes = pb + pat[i];
+                    ENG_TRY(launch_x3_split_planes(t.base, (int)t.cols, (int)t.rows, (int)t.cols, pb + pat[i], e.stream),
+                            "weight planes split");
+                }
+                ENG_TRY(hipStreamSynchronize(e.stream), "weight planes sync");
+            }
+        }
     }
 
     // State: [layer][slot][...] for each of prev, wkv, rosa.

@@ -357,6 +357,140 @@ __device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4
     return *reinterpret_cast<const float4 *>(stage + row * (WN + 4) + 4 * c4);
 }
 
+// Epilogue of the large-tile kernels: waves 4 x 2, wave (wm, wn) owns rows
+// m0 + 64 wm + [0, 64) and columns n0 + (BN / 2) wn + [0, BN / 2), accumulator
+// acc[i][j] the 16 x 16 block (i, j) of it.  `lds` is free when it is called
+// (STAGED: wave-private staging areas of 16 x (BN / 2 + 4) floats).
+template <int BN, bool STAGED>
+__device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)[4][BN / 32], float *lds, int m0,
+                                             int n0, int wave, int lane) {
+    constexpr int WN = BN / 2, NT = WN / 16;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g4 = lane >> 4, li = lane & 15;
+    // Accumulator register r of lane l: row 4 (l / 16) + r, column l % 16 of its 16 x 16 tile.
+    // The parameters are read once, ahead of the LDS fences below (after a
+    // fence the compiler would load each kernel-argument field again).
+    const int M = p.M, ldc = p.ldc, ldr = p.ldr, act = p.act;
+    float *const C = p.C;
+    const float *const bias_p = p.bias, *const res_p = p.residual;
+    if constexpr (STAGED) {
+        // The K loop ended with a barrier: LDS is free.  Wave-private staging areas.
+        constexpr int SW = WN + 4;
+        float *stage = lds + wave * 16 * SW;
+        const int row0 = m0 + wm * 64;
+        if (p.silu_pair) {
+            if constexpr (BN % 128 == 0) {
+                constexpr int HW = WN / 2;  // output columns of the wave
+                const int hcol0 = (n0 + wn * WN) / 2;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                    for (int b = 0; b < WN / 64; ++b)
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
+                                stage[(4 * g4 + r) * SW + 32 * b + 16 * h + li] = x / (1.0f + expf(-x)) * gt;
+                            }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+                    for (int t = 0; t < 16 * HW / 4 / 64; ++t) {
+                        const int q = lane + 64 * t, row = q / (HW / 4), c4 = q % (HW / 4);
+                        const int grow = row0 + i * 16 + row;
+                        if (grow < M)
+                            *reinterpret_cast<float4 *>(C + (size_t)grow * ldc + hcol0 + 4 * c4) =
+                                stage_read<WN>(stage, row, c4);
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                }
+            }
+            return;
+        }
+        const int col0 = n0 + wn * WN;
+        // One copy of the row loop per activation (a uniform branch outside it).
+        auto rows = [&](auto act_c) {
+            constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int j = 0; j < NT; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) stage[(4 * g4 + r) * SW + 16 * j + li] = acc[i][j][r];
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+                for (int t = 0; t < 16 * WN / 4 / 64; ++t) {
+                    const int q = lane + 64 * t, row = q / (WN / 4), c4 = q % (WN / 4);
+                    const int grow = row0 + i * 16 + row, col = col0 + 4 * c4;
+                    if (grow < M) {
+                        float4 x = stage_read<WN>(stage, row, c4);
+                        if (bias_p) {
+                            const float4 b4 = *reinterpret_cast<const float4 *>(bias_p + col);
+                            x.x += b4.x; x.y += b4.y; x.z += b4.z; x.w += b4.w;
+                        }
+                        x.x = apply_act(x.x, ACT); x.y = apply_act(x.y, ACT);
+                        x.z = apply_act(x.z, ACT); x.w = apply_act(x.w, ACT);
+                        if (res_p) {
+                            const float4 r4 = *reinterpret_cast<const float4 *>(res_p + (size_t)grow * ldr + col);
+                            x.x += r4.x; x.y += r4.y; x.z += r4.z; x.w += r4.w;
+                        }
+                        *reinterpret_cast<float4 *>(C + (size_t)grow * ldc + col) = x;
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            }
+        };
+        if (act == ACT_TANH) rows(std::integral_constant<int, ACT_TANH>{});
+        else if (act == ACT_SIGMOID) rows(std::integral_constant<int, ACT_SIGMOID>{});
+        else rows(std::integral_constant<int, ACT_NONE>{});
+        return;
+    }
+    if constexpr (BN % 128 == 0) {
+        if (p.silu_pair) {
+            // Each wave's columns are whole 64-row blocks [32 "in" | 32 "gate"].
+#pragma unroll
+            for (int b = 0; b < WN / 64; ++b)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int hcol = (n0 + wn * WN + 64 * b) / 2 + 16 * h + li;
+                    if (hcol >= p.N / 2) continue;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
+                            if (row < p.M) {
+                                const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
+                                p.C[(size_t)row * p.ldc + hcol] = x / (1.0f + expf(-x)) * gt;
+                            }
+                        }
+                }
+            return;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+        const int col = n0 + wn * WN + j * 16 + li;
+        if (col >= p.N) continue;
+        const float bias = p.bias ? p.bias[col] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
+                if (row < p.M) {
+                    float x = apply_act(acc[i][j][r] + bias, p.act);
+                    if (p.residual) x += p.residual[(size_t)row * p.ldr + col];
+                    p.C[(size_t)row * p.ldc + col] = x;
+                }
+            }
+    }
+}
+
 // X3 (fp32 A and W, K % 32 == 0): each staged fp32 value is split once, when
 // its tile is written to LDS, into three bf16 parts (split3_pair), kept as
 // three bf16 planes of A and of W in one LDS buffer (two barriers per K tile);
@@ -546,116 +680,173 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
         lds_barrier();
     }
 
-    // Accumulator register r of lane l: row 4 (l / 16) + r, column l % 16 of its 16 x 16 tile.
-    if constexpr (STAGED) {
-        // The K loop ended with a barrier: LDS is free.  Wave-private staging areas.
-        constexpr int SW = WN + 4;
-        float *stage = lds + wave * 16 * SW;
-        const int row0 = m0 + wm * 64;
-        if (p.silu_pair) {
-            if constexpr (BN % 128 == 0) {
-                constexpr int HW = WN / 2;  // output columns of the wave
-                const int hcol0 = (n0 + wn * WN) / 2;
+    big_epilogue<BN, STAGED>(p, acc, lds, m0, n0, wave, lane);
+}
+
+// ---------------------------------------------------------------------------
+// X3 with pre-split weight planes (GemmParams::Wp).  The engine splits every
+// fp32 projection matrix once, at creation, into the three bf16 parts the X3
+// form uses (split3_pair), stored as "planes": for each 16-row block rb and
+// 32-k tile kt, three 1-KB blocks (part 1, 2, 3) of 16 rows x 32 bf16, at
+// element ((rb * (K / 32) + kt) * 3 + part) * 512; inside a block, row r's
+// 16-byte chunk c (k 8c .. 8c + 7) sits at r * 32 + 8 (c ^ x3p_swz(r)), which
+// spreads the 16 rows a fragment read touches over all LDS banks.
+//
+// The kernel then never writes LDS from registers: each k tile arrives by
+// direct buffer -> LDS loads (64 lanes x 16 bytes per instruction) into one of
+// two buffers while the MFMAs run on the other -- A as fp32 in 8-row x 32-k
+// blocks (chunk c of row R at c ^ (R & 7) ^ ((R >> 3) & 1), conflict-free for
+// the fragment reads), W as its plane blocks -- with one barrier per k tile.
+// Each wave splits its own 64 A rows into parts (two waves share rows: the
+// split is done twice), W's parts come ready from LDS.  Tile 256 x BN, waves
+// 4 x 2 as in gemm_big_kernel; the per-32-k product order and the split are
+// the X3 form's, so the results are bit-identical to it.  LDS: two buffers of
+// 32 KB (A) + 6 BN / 16 KB (W planes): 160 KB at BN = 256.
+__host__ __device__ constexpr int x3p_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+__device__ __forceinline__ void split3_x8(floatx4 x0, floatx4 x1, bf16x8 &p1, bf16x8 &p2, bf16x8 &p3) {
+    bf16x2 a[4], b[4], c[4];
+    split3_pair(floatx2{x0[0], x0[1]}, a[0], b[0], c[0]);
+    split3_pair(floatx2{x0[2], x0[3]}, a[1], b[1], c[1]);
+    split3_pair(floatx2{x1[0], x1[1]}, a[2], b[2], c[2]);
+    split3_pair(floatx2{x1[2], x1[3]}, a[3], b[3], c[3]);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+    for (int h = 0; h < 4; ++h) {
+        p1[2 * h] = a[h][0]; p1[2 * h + 1] = a[h][1];
+        p2[2 * h] = b[h][0]; p2[2 * h + 1] = b[h][1];
+        p3[2 * h] = c[h][0]; p3[2 * h + 1] = c[h][1];
+    }
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+constexpr uint32_t kWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left free)
+
+template <int BN, bool STAGED>
+__global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int per_xcd) {
+    constexpr int WN = BN / 2, NT = WN / 16;
+    constexpr int AB = kBigBM / 8;       // fp32 A blocks per k tile (8 rows x 32 k = 1 KB)
+    constexpr int WB = BN / 16 * 3;      // W plane blocks per k tile
+    constexpr int NB = AB + WB;          // 1-KB blocks per buffer
+    constexpr int PER = (NB + 7) / 8;    // direct loads per wave and k tile
+    constexpr int GM = 8;                // row tiles walked together (L2 reuse of W inside an XCD)
+    static_assert(2 * NB * 1024 <= 160 * 1024, "two k-tile buffers must fit in LDS");
+    static_assert(2 * NB * 256 >= 8 * 16 * (WN + 4), "LDS too small for the staged epilogue");
+    __shared__ __attribute__((aligned(1024))) float lds[2 * NB * 256];
+
+    const GemmParams &p = g.p[blockIdx.y];
+    const int tiles_n = g.tiles_n[blockIdx.y], total = g.total[blockIdx.y];
+    const int flat = (blockIdx.x % kXcds) * per_xcd + blockIdx.x / kXcds;
+    if (flat >= total) return;
+    const int tiles_m = total / tiles_n;
+    const int grp = flat / (GM * tiles_n), rem = flat - grp * GM * tiles_n;
+    const int gm = min(GM, tiles_m - grp * GM);
+    const int bm = grp * GM + rem % gm, bn = rem / gm;
+    const int m0 = bm * kBigBM, n0 = bn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the LDS destination goes in M0
+    const int wm = wave >> 1, wn = wave & 1;
+    const int g4 = lane >> 4, li = lane & 15;
+    // Kernel-argument fields read once: the loop's direct LDS loads count as
+    // memory writes to the compiler, which would otherwise reload them (a
+    // scalar-memory wait) before every k tile's loads.
+    const int lda = __builtin_amdgcn_readfirstlane(p.lda), K = __builtin_amdgcn_readfirstlane(p.K);
+    const int KT = K / 32;
+    const int rows_a = min(kBigBM, p.M - m0);
+    const auto ra = make_rsrc(p.A + (size_t)m0 * lda, (uint32_t)(((size_t)(rows_a - 1) * lda + K) * 4));
+    const auto rw = make_rsrc(p.Wp, (uint32_t)((size_t)(p.N / 16) * KT * 3 * 1024));
+    const int ar = lane >> 3, apos = lane & 7;  // lane's row / LDS chunk inside an 8-row A block
+
+    auto issue = [&](int kt, int buf) {
 #pragma unroll
-                    for (int b = 0; b < WN / 64; ++b)
-#pragma unroll
-                        for (int h = 0; h < 2; ++h)
-#pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
-                                stage[(4 * g4 + r) * SW + 32 * b + 16 * h + li] = x / (1.0f + expf(-x)) * gt;
-                            }
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-#pragma unroll
-                    for (int t = 0; t < 16 * HW / 4 / 64; ++t) {
-                        const int q = lane + 64 * t, row = q / (HW / 4), c4 = q % (HW / 4);
-                        const int grow = row0 + i * 16 + row;
-                        if (grow < p.M)
-                            *reinterpret_cast<float4 *>(p.C + (size_t)grow * p.ldc + hcol0 + 4 * c4) =
-                                stage_read<WN>(stage, row, c4);
-                    }
-                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-                }
+        for (int i = 0; i < PER; ++i) {
+            const int b = wave + 8 * i;
+            if (b >= NB) break;
+            lds_void_t *dst = (lds_void_t *)(lds + (buf * NB + b) * 256);
+            if (b < AB) {
+                const int c = apos ^ ar ^ (b & 1);
+                const uint32_t off = (uint32_t)(((b * 8 + ar) * lda + kt * 32 + 4 * c) * 4);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, dst, 16, off, 0, 0, 0);
+            } else {
+                const int bb = b - AB, rb = bn * (BN / 16) + bb / 3, part = bb % 3;
+                const uint32_t blk = (uint32_t)(((rb * KT + kt) * 3 + part) * 1024);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, (uint32_t)lane * 16u, blk, 0, 0);
             }
-            return;
         }
-        const int col0 = n0 + wn * WN;
+    };
+
+    floatx4 acc[4][NT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // Fragment offsets: A rows wm 64 + 16 i + li (float index), W rows wn WN + 16 j + li (bf16 index).
+    const int fa = (li & 7) ^ (li >> 3);
+    const int offa0 = (wm * 8 + (li >> 3)) * 256 + (li & 7) * 32 + (((2 * g4) ^ fa) * 4);
+    const int offa1 = (wm * 8 + (li >> 3)) * 256 + (li & 7) * 32 + (((2 * g4 + 1) ^ fa) * 4);
+    const int offw = (AB + wn * NT * 3) * 512 + li * 32 + ((g4 ^ x3p_swz(li)) * 8);
+
+    issue(0, 0);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    lds_barrier();
+    for (int kt = 0; kt < KT; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
+        const float *base = lds + cur * NB * 256;
+        const __bf16 *bh = reinterpret_cast<const __bf16 *>(base);
+        bf16x8 a1[4], a2[4], a3[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int j = 0; j < NT; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) stage[(4 * g4 + r) * SW + 16 * j + li] = acc[i][j][r];
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-#pragma unroll
-            for (int t = 0; t < 16 * WN / 4 / 64; ++t) {
-                const int q = lane + 64 * t, row = q / (WN / 4), c4 = q % (WN / 4);
-                const int grow = row0 + i * 16 + row, col = col0 + 4 * c4;
-                if (grow < p.M) {
-                    float4 x = stage_read<WN>(stage, row, c4);
-                    if (p.bias) {
-                        const float4 b4 = *reinterpret_cast<const float4 *>(p.bias + col);
-                        x.x += b4.x; x.y += b4.y; x.z += b4.z; x.w += b4.w;
-                    }
-                    x.x = apply_act(x.x, p.act); x.y = apply_act(x.y, p.act);
-                    x.z = apply_act(x.z, p.act); x.w = apply_act(x.w, p.act);
-                    if (p.residual) {
-                        const float4 r4 = *reinterpret_cast<const float4 *>(p.residual + (size_t)grow * p.ldr + col);
-                        x.x += r4.x; x.y += r4.y; x.z += r4.z; x.w += r4.w;
-                    }
-                    *reinterpret_cast<float4 *>(p.C + (size_t)grow * p.ldc + col) = x;
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            const floatx4 x0 = *reinterpret_cast<const floatx4 *>(base + offa0 + i * 512);
+            const floatx4 x1 = *reinterpret_cast<const floatx4 *>(base + offa1 + i * 512);
+            split3_x8(x0, x1, a1[i], a2[i], a3[i]);
         }
-        return;
-    }
-    if constexpr (BN % 128 == 0) {
-        if (p.silu_pair) {
-            // Each wave's columns are whole 64-row blocks [32 "in" | 32 "gate"].
+        bf16x8 nw1 = *reinterpret_cast<const bf16x8 *>(bh + offw);
+        bf16x8 nw2 = *reinterpret_cast<const bf16x8 *>(bh + offw + 512);
+        bf16x8 nw3 = *reinterpret_cast<const bf16x8 *>(bh + offw + 1024);
 #pragma unroll
-            for (int b = 0; b < WN / 64; ++b)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int hcol = (n0 + wn * WN + 64 * b) / 2 + 16 * h + li;
-                    if (hcol >= p.N / 2) continue;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int r = 0; r < 4; ++r) {
-                            const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
-                            if (row < p.M) {
-                                const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
-                                p.C[(size_t)row * p.ldc + hcol] = x / (1.0f + expf(-x)) * gt;
-                            }
-                        }
-                }
-            return;
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-        const int col = n0 + wn * WN + j * 16 + li;
-        if (col >= p.N) continue;
-        const float bias = p.bias ? p.bias[col] : 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
-                if (row < p.M) {
-                    float x = apply_act(acc[i][j][r] + bias, p.act);
-                    if (p.residual) x += p.residual[(size_t)row * p.ldr + col];
-                    p.C[(size_t)row * p.ldc + col] = x;
-                }
+        for (int j = 0; j < NT; ++j) {
+            const bf16x8 w1 = nw1, w2 = nw2, w3 = nw3;
+            if (j + 1 < NT) {
+                const __bf16 *bp = bh + offw + (j + 1) * 1536;
+                nw1 = *reinterpret_cast<const bf16x8 *>(bp);
+                nw2 = *reinterpret_cast<const bf16x8 *>(bp + 512);
+                nw3 = *reinterpret_cast<const bf16x8 *>(bp + 1024);
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                floatx4 c = acc[i][j];
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[i], w1, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w3, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[i], w2, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[i], w1, c, 0, 0, 0);
+                c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w2, c, 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w1, c, 0, 0, 0);
+            }
+        }
+        // This wave's loads of the next tile have landed; after the barrier
+        // every wave's have, and nobody reads this tile's buffer any more.
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        lds_barrier();
     }
+    big_epilogue<BN, STAGED>(p, acc, lds, m0, n0, wave, lane);
+}
+
+// fp32 W [N][ldw] -> X3 planes (layout above): one thread per 8 consecutive k of a row.
+__global__ void x3_split_planes_kernel(const float *W, int ldw, int N, int K, uint16_t *planes) {
+    const int chunks = K / 8;
+    const long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= (long long)N * chunks) return;
+    const int n = (int)(q / chunks), c8 = (int)(q % chunks);
+    const float *src = W + (size_t)n * ldw + 8 * c8;
+    const floatx4 x0 = *reinterpret_cast<const floatx4 *>(src), x1 = *reinterpret_cast<const floatx4 *>(src + 4);
+    bf16x8 p1, p2, p3;
+    split3_x8(x0, x1, p1, p2, p3);
+    const int rb = n / 16, r = n % 16, kt = c8 / 4, c = c8 % 4;
+    uint16_t *dst = planes + ((size_t)(rb * (K / 32) + kt) * 3) * 512 + r * 32 + ((c ^ x3p_swz(r)) * 8);
+    *reinterpret_cast<bf16x8 *>(dst) = p1;
+    *reinterpret_cast<bf16x8 *>(dst + 512) = p2;
+    *reinterpret_cast<bf16x8 *>(dst + 1024) = p3;
 }
 
 // ---------------------------------------------------------------------------
@@ -1443,6 +1634,27 @@ void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStre
         hipLaunchKernelGGL((gemm_big_kernel<BN, false, WB, X3>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
 }
 
+template <int BN>
+void launch_x3p(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStream_t stream) {
+    if (staged)
+        hipLaunchKernelGGL((gemm_x3p_kernel<BN, true>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+    else
+        hipLaunchKernelGGL((gemm_x3p_kernel<BN, false>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+}
+
+// The X3 form from pre-split weight planes when every product of the group
+// has them and its A rows can be loaded straight into LDS (16-byte aligned
+// rows); otherwise gemm_big_kernel splits W itself.
+bool use_x3p(const GemmGroup &g, int n) {
+    for (int i = 0; i < n; ++i) {
+        const GemmParams &p = g.p[i];
+        if (!p.Wp || p.K % 32 != 0 || p.N % 16 != 0 || p.lda % 4 != 0 ||
+            (reinterpret_cast<uintptr_t>(p.A) & 15) != 0 || x3_planes_elems(p.N, p.K) * 2 >= (1ull << 32))
+            return false;
+    }
+    return true;
+}
+
 // fp32 products on the bf16 matrix cores through three-part splits (the X3
 // form of gemm_big_kernel) when every K of the group is a multiple of 32;
 // YUF_GEMM_X3=0 keeps the fp32 MFMA form.
@@ -1769,6 +1981,15 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
             staged = staged && (bits & 15) == 0 && p.ldc % 4 == 0 && (!p.residual || p.ldr % 4 == 0);
         }
         const dim3 grid(per_xcd * kXcds, n), block(kBigThreads);
+        if (use_x3(g, n) && use_x3p(g, n)) {
+            switch (bn) {
+                case 256: launch_x3p<256>(g, per_xcd, staged, grid, stream); break;
+                case 160: launch_x3p<160>(g, per_xcd, staged, grid, stream); break;
+                case 128: launch_x3p<128>(g, per_xcd, staged, grid, stream); break;
+                default: launch_x3p<64>(g, per_xcd, staged, grid, stream); break;
+            }
+            return hipGetLastError();
+        }
         if (use_x3(g, n)) {
             switch (bn) {
                 case 256: launch_big<256, false, true>(g, per_xcd, staged, grid, stream); break;
@@ -1793,6 +2014,21 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
 
 size_t gemm_workspace_floats(int N, int K) { return (size_t)skinny_splits(N, K) * 64 * N; }
 
+size_t x3_planes_elems(int N, int K) {
+    if (N <= 0 || K <= 0 || N % 16 != 0 || K % 32 != 0) return 0;
+    return (size_t)N * K * 3;
+}
+
+hipError_t launch_x3_split_planes(const float *W, int ldw, int N, int K, uint16_t *planes, hipStream_t stream) {
+    if (!x3_planes_elems(N, K) || ldw < K || ldw % 4 != 0 || !W || !planes ||
+        (reinterpret_cast<uintptr_t>(W) & 15) != 0 || (reinterpret_cast<uintptr_t>(planes) & 15) != 0)
+        return hipErrorInvalidValue;
+    const long long items = (long long)N * (K / 8);
+    hipLaunchKernelGGL(x3_split_planes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, W, ldw, N,
+                       K, planes);
+    return hipGetLastError();
+}
+
 }  // namespace yuf
 
 extern "C" int yuf_linear_f32(int M, int N, int K, const float *A, const float *W, const float *bias, int act,
@@ -1806,6 +2042,36 @@ extern "C" int yuf_linear_f32(int M, int N, int K, const float *A, const float *
     p.bias = bias; p.act = act; p.residual = residual; p.ldr = N;
     hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
     if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("linear launch: ") + hipGetErrorString(err));
+    return YUF_OK;
+}
+
+extern "C" size_t yuf_x3_planes_elems(int N, int K) { return yuf::x3_planes_elems(N, K); }
+
+extern "C" int yuf_x3_split_planes(int N, int K, const float *W, uint16_t *planes, void *stream) {
+    using namespace yuf;
+    if (!x3_planes_elems(N, K)) return fail(YUF_ERR_INVALID, "x3_split_planes: needs N % 16 == 0, K % 32 == 0");
+    if (!W || !planes) return fail(YUF_ERR_INVALID, "x3_split_planes: null pointer");
+    if ((reinterpret_cast<uintptr_t>(W) & 15) != 0 || (reinterpret_cast<uintptr_t>(planes) & 15) != 0)
+        return fail(YUF_ERR_INVALID, "x3_split_planes: W and planes must be 16-byte aligned");
+    hipError_t err = launch_x3_split_planes(W, K, N, K, planes, static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("x3_split_planes launch: ") + hipGetErrorString(err));
+    return YUF_OK;
+}
+
+extern "C" int yuf_linear_f32_planes(int M, int N, int K, const float *A, const float *W, const uint16_t *Wp,
+                                     const float *bias, int act, const float *residual, float *C, void *stream) {
+    using namespace yuf;
+    if (M < 0 || N < 0 || K < 1) return fail(YUF_ERR_INVALID, "linear_planes: bad sizes");
+    if (act < ACT_NONE || act > ACT_SIGMOID) return fail(YUF_ERR_INVALID, "linear_planes: bad activation");
+    if (M > 0 && N > 0 && (!A || !W || !Wp || !C)) return fail(YUF_ERR_INVALID, "linear_planes: null pointer");
+    if (M > 0 && N > 0 && !x3_planes_elems(N, K))
+        return fail(YUF_ERR_INVALID, "linear_planes: planes need N % 16 == 0, K % 32 == 0");
+    GemmParams p;
+    p.M = M; p.N = N; p.K = K; p.A = A; p.lda = K; p.W = W; p.ldw = K; p.C = C; p.ldc = N;
+    p.bias = bias; p.act = act; p.residual = residual; p.ldr = N;
+    if (M > 64) p.Wp = Wp;
+    hipError_t err = launch_gemm(p, static_cast<hipStream_t>(stream));
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("linear_planes launch: ") + hipGetErrorString(err));
     return YUF_OK;
 }
 

@@ -123,6 +123,11 @@ struct GemmParams {
     const float *Wt = nullptr;
     const uint16_t *Wht = nullptr;
     int wt_ld = 0;
+    // Optional pre-split copy of an fp32 W for the large-tile X3 products
+    // (M > 64): its three bf16 parts in the plane layout of
+    // launch_x3_split_planes (N % 16 == 0, K % 32 == 0).  Same results as
+    // without it.
+    const uint16_t *Wp = nullptr;
     // Decode kernels only: A (and a_gate) stored in 16 x 16 tiles (tile_index,
     // row strides lda / ldg), and, for the SiLU-pair product, C written that way
     // (row stride ldc).  A tiled A needs one round of k steps per wave.
@@ -165,6 +170,11 @@ constexpr int kMaxGroup = 6;
 hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream);
 // Workspace the short-M path can use for an N-column product (floats).
 size_t gemm_workspace_floats(int N, int K);
+// Pre-split weight planes (GemmParams::Wp): elements (uint16) for an [N, K]
+// matrix, 0 unless N % 16 == 0 and K % 32 == 0; the split of fp32 W [N][ldw]
+// (16-byte aligned, ldw % 4 == 0) into them.
+size_t x3_planes_elems(int N, int K);
+hipError_t launch_x3_split_planes(const float *W, int ldw, int N, int K, uint16_t *planes, hipStream_t stream);
 
 // --------------------------------------------------- persistent decode layer
 // One decode layer (T = 1) of up to kDlRows streams per XCD group in one
