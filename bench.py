@@ -118,13 +118,37 @@ def decode_step_bytes(cfg, streams: int) -> int:
     return 4 * (params + 2 * streams * state + streams * cfg.vocab_size)
 
 
-def decode_roofline(cfg, streams: int, ms_per_step: float, operator_leg: dict) -> dict:
+def wkv_step_in_model_bytes(cfg, n: int) -> int:
+    """Algorithmic bytes of one in-model WKV-7 step launch (the fused form
+    with the second low-rank stage) for n streams: per stream the state read
+    and written (8 B x H N^2), r, k, v and the three rank-L rows read, y and
+    the output gate written; once per launch w2t / a2t / g2t ([d, L] each)
+    and w0, a0, k_k, k_a ([d] each)."""
+    d, L, hn2 = cfg.d_model, cfg.low_rank, cfg.n_heads * cfg.head_size ** 2
+    per_stream = 8 * hn2 + 12 * d + 12 * L + 8 * d
+    return n * per_stream + 12 * d * L + 16 * d
+
+
+def wkv_step_in_model(engine, cfg, iters: int = 50) -> dict:
+    """The decode step's own WKV-7 kernel (wkv7_step_kernel<N,true,4,true>,
+    low-rank stage folded in, the first layer of the last step's stream
+    group), relaunched alone with its inputs and timed with HIP events on the
+    engine's stream (yuf_engine_time_wkv_step)."""
+    us, n = engine.time_wkv_step(iters)
+    nbytes = wkv_step_in_model_bytes(cfg, n)
+    achieved = nbytes / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "avg_us": round(us, 2), "streams": n,
+            "algorithmic_bytes": nbytes,
+            "kernel": f"wkv7_step_kernel<{cfg.head_size},true,4,true> (in-model, {n} streams, low-rank stage folded in)"}
+
+
+def decode_roofline(cfg, streams: int, ms_per_step: float, operator_leg: dict, in_model: dict = None) -> dict:
     """The whole decode step against the HBM roofline: algorithmic bytes per
     step / measured step time (the step is a chain of dependent launches, so
-    this is the figure to move); beside it the operator-form WKV-7 step kernel
-    timed alone (wkv7_step_kernel<N,false,1,false> through yuf_wkv7_scan_f32,
-    not the in-model variant with the low-rank stage folded in, which only runs
-    inside the replayed step graph -- see profiles/decode_c4_kernel_stats.md)."""
+    this is the figure to move); beside it the step's own WKV-7 kernel timed
+    alone (in_model) and the operator-form WKV-7 step kernel
+    (wkv7_step_kernel<N,false,1,false> through yuf_wkv7_scan_f32)."""
     nbytes = decode_step_bytes(cfg, streams)
     achieved = nbytes / (ms_per_step * 1e-3) / 1e9
     traffic = None
@@ -135,7 +159,8 @@ def decode_roofline(cfg, streams: int, ms_per_step: float, operator_leg: dict) -
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": f"whole C4 decode step ({streams} streams, 0.1B model, graph-replayed)",
-            "algorithmic_bytes": nbytes, "ms_per_step": round(ms_per_step, 4), "wkv_step_operator": operator_leg}
+            "algorithmic_bytes": nbytes, "ms_per_step": round(ms_per_step, 4), "wkv_step_in_model": in_model,
+            "wkv_step_operator": operator_leg}
 
 
 def bench_wkv_step(iters: int) -> dict:
@@ -489,9 +514,11 @@ def main() -> int:
     dec_elapsed = time.perf_counter() - t0
     decode_tps = S * args.decode_steps / dec_elapsed
     log(f"decode {dec_elapsed * 1e3 / args.decode_steps:.3f} ms/step, {decode_tps:.0f} tokens/s")
+    wkv_in_model = wkv_step_in_model(engine, cfg)
+    log(f"in-model WKV step {wkv_in_model['avg_us']} us ({wkv_in_model['frac']:.3f} of HBM)")
     if args.only == "decode":
-        print(json.dumps({"decode_tokens_per_s": decode_tps, "decode_ms_per_step": dec_elapsed * 1e3 / args.decode_steps}),
-              flush=True)
+        print(json.dumps({"decode_tokens_per_s": decode_tps, "decode_ms_per_step": dec_elapsed * 1e3 / args.decode_steps,
+                          "wkv_step_in_model": wkv_in_model}), flush=True)
         return 0
     engine.close()
     del logits
@@ -546,7 +573,7 @@ def main() -> int:
         "decode_tokens_per_s": round(decode_tps, 1),
         "decode_ms_per_step": round(dec_elapsed * 1e3 / args.decode_steps, 3),
         "roofline": roofline,
-        "decode_roofline": decode_roofline(cfg, S, dec_elapsed * 1e3 / args.decode_steps, step),
+        "decode_roofline": decode_roofline(cfg, S, dec_elapsed * 1e3 / args.decode_steps, step, wkv_in_model),
         "rosa_roofline": rosa,
         "gemm_roofline": gemm,
         "cpu_baseline": cpu,

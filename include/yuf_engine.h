@@ -302,6 +302,19 @@ int yuf_step_device(yuf_engine *eng, int n, const int32_t *slots, const int32_t 
  * the reference, whose engine takes host token ids only (model.rs:54-60). */
 int yuf_engine_take_error(yuf_engine *eng);
 
+/*
+ * Measurement hook (no reference counterpart): times the decode step's
+ * first-layer WKV-7 step kernel -- the fused form with the second low-rank
+ * stage, as the last decode step launched it (same inputs, streams and
+ * launch shape) -- `iters` times on the engine's stream between HIP events,
+ * writing the new state to a scratch buffer so the engine's state does not
+ * change.  *avg_us receives the mean duration, *streams (if not NULL) the
+ * number of streams of that launch.  Needs a prior decode step with fp32
+ * weights and the fused low-rank step (else YUF_ERR_INVALID); allocates and
+ * frees its scratch.
+ */
+int yuf_engine_time_wkv_step(yuf_engine *eng, int iters, float *avg_us, int *streams);
+
 /* Zero all recurrent state of one slot (slot = -1: every slot), including
  * the token-shift `previous` vector the reference reset leaves stale
  * (Model::reset_state, model.rs:62-65). */

@@ -934,3 +934,33 @@ def test_c5_as_configured_32x8192_then_512_steps(tmp_path):
             worst = max(worst, _c5_check(g[[5, 17]], r.numpy(), 2e-2, f"step {t}"))
     print(f"C5 decode, streams 5 and 17 over {follow} steps: worst deviation {worst:.2e}; {steps} steps run",
           flush=True)
+
+
+def test_time_wkv_step_leaves_the_state_alone(tmp_path):
+    """yuf_engine_time_wkv_step (the measurement hook bench.py uses for the
+    in-model WKV-7 step kernel): refused before any decode step; afterwards it
+    relaunches the first layer's step kernel with the step's own inputs, and
+    the engine's saved state and the next step's logits are exactly what they
+    would have been without it."""
+    from yufmusicgen_amd._lib import YufError
+    cfg = PRESETS["0.1b"]
+    path = tmp_path / "m.yuf"
+    write_yuf(path, cfg, synth_weights(cfg, seed=31))
+    ck = Checkpoint.load(path)
+    tokens = uniform_tokens(32, 64, 16, cfg.vocab_size)
+    outs = []
+    for probe in (False, True):
+        eng = Engine(ck, max_streams=64, max_tokens=64 * 16)
+        if probe:
+            with pytest.raises(YufError):
+                eng.time_wkv_step(5)
+        eng.prefill(tokens)
+        eng.step(tokens[:, 0])
+        if probe:
+            us, n = eng.time_wkv_step(20)
+            print(f"in-model WKV step: {us:.2f} us for {n} streams", flush=True)
+            assert us > 0 and n in (32, 64)
+        outs.append((_states_from_blob(eng, list(range(64))), eng.step(tokens[:, 1])))
+        eng.close()
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)

@@ -49,6 +49,8 @@ SIGNATURES = {
     "yuf_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_ln_linear_f32": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 9),
     "yuf_x3_planes_elems": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int]),
+    "yuf_engine_time_wkv_step": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_float),
+                                                ctypes.POINTER(ctypes.c_int)]),
     "yuf_x3_split_planes": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, c_void_p]),
     "yuf_linear_f32_planes": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 4 + [ctypes.c_int] + [c_void_p] * 3),
     "yuf_linear_bf16w": (ctypes.c_int, [ctypes.c_int] * 3 + [c_void_p] * 3 + [ctypes.c_int] + [c_void_p] * 3),

@@ -104,6 +104,10 @@ struct Engine {
     int *dl_sync = nullptr;          // per-layer counter blocks, zeroed at the start of each step
     size_t dl_sync_ints = 0;         // per layer
     int prefill_groups = 0;                                    // YUF_PREFILL_GROUPS=1..4: streams for the batch's parts (0: automatic)
+    // The first layer's WKV-7 step launch of the last decode pass (fused
+    // low-rank form), kept for yuf_engine_time_wkv_step.
+    WkvParams wkv_probe;
+    bool wkv_probe_set = false;
     float *gemm_ws = nullptr;  // split-K partials of short-M (decode) products
     size_t gemm_ws_floats = 0;
     // Out-of-range token flags set by the embedding kernel: bad_host for the
@@ -628,6 +632,10 @@ int forward_pass(Engine &e, const Act &a, int n, int Tc, float *logits, int mode
             wp.tiled_out = tl;
         }
         ENG_TRY(launch_wkv7(wp, s.head_size, true, st), "wkv7");
+        if (fuse_lr && l == 0) {
+            e.wkv_probe = wp;
+            e.wkv_probe_set = true;
+        }
         if ((rc = ln_gemm(e, st, M, d, d, a.y, d, w.ln_o_w, w.ln_o_b, a.g, a.z, w.w_o, a.h, d, nullptr, a.h, d, false,
                           tl)) != YUF_OK)
             return rc;
@@ -1305,6 +1313,36 @@ extern "C" int yuf_prefill(yuf_engine *eng, int n, const int32_t *slots, int T, 
         if (bad & 2) return fail(YUF_ERR_HIP, kDecodeLayerTimeout);
         return fail(YUF_ERR_RANGE, "a token id was out of range on the device (its embedding was zeroed)");
     }
+    return YUF_OK;
+}
+
+extern "C" int yuf_engine_time_wkv_step(yuf_engine *eng, int iters, float *avg_us, int *streams) {
+    using namespace yuf;
+    if (!eng || !avg_us || iters < 1) return fail(YUF_ERR_INVALID, "time_wkv_step: bad arguments");
+    Engine &e = eng->e;
+    if (!e.wkv_probe_set) return fail(YUF_ERR_INVALID, "time_wkv_step: no decode step has run the fused WKV-7 step yet");
+    // Same launch as the step's first layer, but the new state goes to a
+    // scratch copy, so the engine's state is not advanced.
+    WkvParams wp = e.wkv_probe;
+    const size_t floats = (size_t)e.max_streams * e.wkv_floats();
+    DeviceBuf scratch;
+    ENG_TRY(hipMalloc(&scratch.p, floats * sizeof(float)), "time_wkv_step scratch");
+    wp.state_out = static_cast<float *>(scratch.p);
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    ENG_TRY(hipEventCreate(&t0), "event");
+    hipError_t err = hipEventCreate(&t1);
+    if (err == hipSuccess) err = launch_wkv7(wp, e.s.head_size, true, e.stream);  // warm-up
+    if (err == hipSuccess) err = hipEventRecord(t0, e.stream);
+    for (int i = 0; i < iters && err == hipSuccess; ++i) err = launch_wkv7(wp, e.s.head_size, true, e.stream);
+    if (err == hipSuccess) err = hipEventRecord(t1, e.stream);
+    if (err == hipSuccess) err = hipEventSynchronize(t1);
+    float ms = 0.f;
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, t0, t1);
+    hipEventDestroy(t0);
+    if (t1) hipEventDestroy(t1);
+    if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("time_wkv_step: ") + hipGetErrorString(err));
+    *avg_us = ms * 1e3f / iters;
+    if (streams) *streams = wp.B;
     return YUF_OK;
 }
 

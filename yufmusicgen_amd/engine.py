@@ -185,6 +185,14 @@ class Engine:
         last check (``yuf_engine_take_error``; synchronises the engine stream)."""
         check(lib().yuf_engine_take_error(self._h))
 
+    def time_wkv_step(self, iters: int = 50):
+        """Mean duration (us) and stream count of the last decode step's
+        first-layer WKV-7 step kernel, relaunched alone ``iters`` times with its
+        own inputs (``yuf_engine_time_wkv_step``; the engine state is unchanged)."""
+        us, n = ctypes.c_float(), ctypes.c_int()
+        check(lib().yuf_engine_time_wkv_step(self._h, iters, ctypes.byref(us), ctypes.byref(n)))
+        return float(us.value), int(n.value)
+
     def close(self) -> None:
         if self._h:
             lib().yuf_engine_destroy(self._h)
