@@ -65,6 +65,38 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Column j of A^L, A = diag(lambda) (I - 2 u u^T) (lambda post-sigmoid, u
+// unit), in double, by one wave: A applied L times to e_j through the
+// rank-one form A x = lambda (x - 2 (u.x) u); AL[i][j] = x_i.  PER =
+// ceil(D / 64) rows per lane; the L projections u.x are the chain, each one
+// DPP / row-swap reduction.
+template <int PER>
+__device__ __forceinline__ void power_column(int D, int L, const float *lambda, const float *u, float *AL, int j,
+                                             int lane) {
+    double x[PER], uu[PER], lam[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int i = lane + 64 * e;
+        const bool in = i < D;
+        x[e] = in && i == j ? 1.0 : 0.0;
+        uu[e] = in ? (double)u[i] : 0.0;
+        lam[e] = in ? (double)lambda[i] : 0.0;
+    }
+    for (int step = 0; step < L; ++step) {
+        double pr = 0.0;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) pr += uu[e] * x[e];
+        pr = wave_sum_f64(pr);
+#pragma unroll
+        for (int e = 0; e < PER; ++e) x[e] = lam[e] * (x[e] - 2.0 * pr * uu[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const int i = lane + 64 * e;
+        if (i < D) AL[(size_t)i * D + j] = (float)x[e];
+    }
+}
+
 // EMIT = false: end states only (the first pass of the segmented scan), so
 // neither the reads nor their gate are computed and the gate input is not
 // loaded.  A compile-time switch: as a run-time flag its tests inside the
@@ -417,67 +449,94 @@ __global__ void __launch_bounds__(256) rosa_step_kernel(RosaParams p) {
 // the state after segment s of length L is m_{s+1} = A^L m_s + z_s, where z_s
 // is the segment's end state from a zero start.  One workgroup per chain walks
 // its P segments: it records each segment's start state (carry) and applies
-// A^L (row-major [D][D], each thread holding 64 entries of one row in
-// registers) plus z_s.  D in {64, 128, 256}: blockDim = D * D / 64.
-__global__ void __launch_bounds__(1024) rosa_carry_kernel(int P, int D, const float *AL, const float *z,
-                                                          const float *memory_in, const int *slot, float *carry) {
-    __shared__ float st[256];
+// A^L (row-major [D][D]) plus z_s.  D in {64, 128, 256}: blockDim = D * D / 64;
+// thread (h, r) = (tid / D, tid % D) keeps the 64 entries of row r in column
+// block h in registers, so the 64 lanes of a wave read the same 64 state
+// values (LDS broadcasts).  The P steps are the chain, so a step only touches
+// registers and LDS: the z rows are staged into LDS in blocks before the
+// steps that use them (a wait for a global load would also wait for every
+// carry store still in flight -- a memory round trip per step), the 64 state
+// values are read before the FMAs (four independent chains), and the column
+// blocks' partial sums meet in LDS in a fixed order.  Measured at the C3
+// layer shape (P = 32, D = 128): 21.5 -> 16.6 us.
+template <int D>
+__global__ void __launch_bounds__(D * D / 64) rosa_carry_kernel(int P, const float *AL, const float *z,
+                                                                const float *memory_in, const int *slot, float *carry) {
+    constexpr int kZFloats = 16384;  // staged z rows (64 KB)
+    constexpr int nthr = D * D / 64, nb = D / 64;
+    __shared__ __attribute__((aligned(16))) float st[2][D];
+    __shared__ float part[nb][D];
+    __shared__ __attribute__((aligned(16))) float zs[kZFloats];
     const int b = blockIdx.x, tid = threadIdx.x;
-    const int tpr = D / 64, r = tid / tpr, q = tid - r * tpr;
+    const int h = tid / D, r = tid - h * D;
     float arow[64];
+    const float4 *arow4 = reinterpret_cast<const float4 *>(AL + (size_t)r * D + h * 64);
 #pragma unroll
-    for (int j = 0; j < 64; ++j) arow[j] = AL[(size_t)r * D + q * 64 + j];
+    for (int j = 0; j < 16; ++j) {
+        const float4 a4 = arow4[j];
+        arow[4 * j] = a4.x; arow[4 * j + 1] = a4.y; arow[4 * j + 2] = a4.z; arow[4 * j + 3] = a4.w;
+    }
     const int sl = slot ? slot[b] : b;
-    if (tid < D) st[tid] = memory_in ? memory_in[(size_t)sl * D + tid] : 0.0f;
-    // LDS-only barriers: the carry stores below stay in flight across them.
-    lds_barrier();
-    for (int s = 0; s < P; ++s) {
-        const size_t v = (size_t)b * P + s;
-        if (tid < D) carry[v * D + tid] = st[tid];
-        const float zr = q == 0 ? z[v * D + r] : 0.0f;
-        float dot = 0.0f;
+    if (tid < D) st[0][tid] = memory_in ? memory_in[(size_t)sl * D + tid] : 0.0f;
+    constexpr int zb = kZFloats / D;  // steps per staged block
+    for (int s0 = 0; s0 < P; s0 += zb) {
+        const int n = min(zb, P - s0);
+        const float4 *z4 = reinterpret_cast<const float4 *>(z + ((size_t)b * P + s0) * D);
+        float4 *zs4 = reinterpret_cast<float4 *>(zs);
+        const int total4 = n * D / 4;
+        for (int i0 = 0; i0 < total4; i0 += 8 * nthr) {  // eight loads in flight per thread
+            float4 t4[8];
 #pragma unroll
-        for (int j = 0; j < 64; ++j) dot = fmaf(arow[j], st[q * 64 + j], dot);
-        // the tpr partial dot products of a row sit in adjacent lanes
-        for (int o = 1; o < tpr; o <<= 1) dot += __shfl_xor(dot, o);
+            for (int u = 0; u < 8; ++u) t4[u] = z4[min(i0 + u * nthr + tid, total4 - 1)];  // in bounds; extras unused
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = i0 + u * nthr + tid;
+                if (i < total4) zs4[i] = t4[u];
+            }
+        }
+        // LDS-only barriers: the carry stores below stay in flight across them.
         lds_barrier();
-        if (q == 0) st[r] = dot + zr;
-        lds_barrier();
+        for (int k = 0; k < n; ++k) {
+            const int s = s0 + k, cur = s & 1;
+            const size_t v = (size_t)b * P + s;
+            if (tid < D) carry[v * D + tid] = st[cur][tid];
+            float x[64];
+            const float4 *x4 = reinterpret_cast<const float4 *>(st[cur] + h * 64);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float4 t = x4[j];
+                x[4 * j] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
+            }
+            float d4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 64; j += 4)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) d4[q] = fmaf(arow[j + q], x[j + q], d4[q]);
+            const float dot = (d4[0] + d4[1]) + (d4[2] + d4[3]);
+            if constexpr (nb == 1) {
+                st[cur ^ 1][r] = dot + zs[k * D + r];
+            } else {
+                part[h][r] = dot;
+                lds_barrier();
+                if (h == 0) {
+                    float sum = part[0][r];
+#pragma unroll
+                    for (int q = 1; q < nb; ++q) sum += part[q][r];
+                    st[cur ^ 1][r] = sum + zs[k * D + r];
+                }
+            }
+            lds_barrier();
+        }
     }
 }
 
-// A^L of the ROSA transition A = diag(lambda) (I - 2 u u^T) for the operator
-// path (lambda post-sigmoid, u unit), in double precision like the engine's
-// host-side copy: wave w of workgroup g applies A L times to e_j, j = 4 g + w,
-// through the rank-one form A x = lambda (x - 2 (u.x) u); AL[i][j] = x_i.
-// PER = ceil(D / 64) rows per lane; the L projections u.x are the chain, each
-// one DPP / row-swap reduction.
+// A^L of the ROSA transition for the operator path on its own (lambda
+// post-sigmoid, u unit): wave w of workgroup g computes column 4 g + w.
 template <int PER>
 __global__ void __launch_bounds__(256) rosa_power_kernel(int D, int L, const float *lambda, const float *u, float *AL) {
     const int j = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (j >= D) return;  // uniform over the wave
-    double x[PER], uu[PER], lam[PER];
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-        const int i = lane + 64 * e;
-        const bool in = i < D;
-        x[e] = in && i == j ? 1.0 : 0.0;
-        uu[e] = in ? (double)u[i] : 0.0;
-        lam[e] = in ? (double)lambda[i] : 0.0;
-    }
-    for (int step = 0; step < L; ++step) {
-        double pr = 0.0;
-#pragma unroll
-        for (int e = 0; e < PER; ++e) pr += uu[e] * x[e];
-        pr = wave_sum_f64(pr);
-#pragma unroll
-        for (int e = 0; e < PER; ++e) x[e] = lam[e] * (x[e] - 2.0 * pr * uu[e]);
-    }
-#pragma unroll
-    for (int e = 0; e < PER; ++e) {
-        const int i = lane + 64 * e;
-        if (i < D) AL[(size_t)i * D + j] = (float)x[e];
-    }
+    power_column<PER>(D, L, lambda, u, AL, j, lane);
 }
 
 hipError_t launch_rosa_power(int D, int L, const float *lambda, const float *u, float *AL, hipStream_t stream) {
@@ -508,8 +567,11 @@ hipError_t launch_rosa_segmented(const RosaParams &p, const float *AL, int L, fl
     hipError_t e = launch_rosa(a, stream);
     if (e != hipSuccess) return e;
     // 2. chain the segment start states.
-    hipLaunchKernelGGL(rosa_carry_kernel, dim3(p.B), dim3(p.D * p.D / 64), 0, stream, P, p.D, AL, z, p.memory_in,
-                       p.slot, carry);
+    switch (p.D) {
+        case 64: hipLaunchKernelGGL(rosa_carry_kernel<64>, dim3(p.B), dim3(64), 0, stream, P, AL, z, p.memory_in, p.slot, carry); break;
+        case 128: hipLaunchKernelGGL(rosa_carry_kernel<128>, dim3(p.B), dim3(256), 0, stream, P, AL, z, p.memory_in, p.slot, carry); break;
+        default: hipLaunchKernelGGL(rosa_carry_kernel<256>, dim3(p.B), dim3(1024), 0, stream, P, AL, z, p.memory_in, p.slot, carry); break;
+    }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // 3. every segment again from its true start: the reads, and the last
     // segment's end state as the chain's new state.
@@ -662,6 +724,8 @@ int rosa_operator(int B, int T, int D, const float *cand, const float *write, co
             return fail(YUF_ERR_OOM, std::string("rosa scratch: ") + hipGetErrorString(err));
         }
         float *AL = buf, *z = AL + (size_t)D * D, *carry = z + seg;
+        // A^L in its own launch (as extra workgroups of the first pass it
+        // measured no faster: 21.2-21.4 us against 8.5 + 13.9 us).
         err = launch_rosa_power(D, kOpRosaSeg, decay, direction, AL, st);
         if (err == hipSuccess) err = launch_rosa_segmented(p, AL, kOpRosaSeg, z, carry, st);
     } else {
