@@ -454,11 +454,13 @@ __global__ void __launch_bounds__(256) rosa_step_kernel(RosaParams p) {
 // block h in registers, so the 64 lanes of a wave read the same 64 state
 // values (LDS broadcasts).  The P steps are the chain, so a step only touches
 // registers and LDS: the z rows are staged into LDS in blocks before the
-// steps that use them (a wait for a global load would also wait for every
-// carry store still in flight -- a memory round trip per step), the 64 state
-// values are read before the FMAs (four independent chains), and the column
-// blocks' partial sums meet in LDS in a fixed order.  Measured at the C3
-// layer shape (P = 32, D = 128): 21.5 -> 16.6 us.
+// steps that use them (no global-load wait inside the chain, which would also
+// wait for the carry stores in flight), the 64 state values are read before
+// the FMAs (four independent chains), and the column blocks' partial sums
+// meet in LDS in a fixed order.  Measured at the C3 layer shape (P = 32, D =
+// 128): 21.5 -> 16.6 us, all of it from the launch bounds sized to the
+// workgroup (the compiler had capped registers for 1024 threads and kept one
+// or two state reads in flight); the z staging alone changed nothing.
 template <int D>
 __global__ void __launch_bounds__(D * D / 64) rosa_carry_kernel(int P, const float *AL, const float *z,
                                                                 const float *memory_in, const int *slot, float *carry) {
