@@ -107,7 +107,7 @@ def bench_scan(iters: int) -> dict:
 
 
 def decode_step_bytes(cfg, streams: int) -> int:
-    """Algorithmic HBM bytes of one decode step (SURVEY-style count): every
+    """Algorithmic HBM bytes of one decode step: every
     weight once (the tied embedding once, as the LM head; the gathered rows are
     negligible), each stream's recurrent state read and written (previous, WKV,
     ROSA), and the V logits written.  0.1B model, 64 streams: 646.5 MB."""
