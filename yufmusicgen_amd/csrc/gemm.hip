@@ -361,8 +361,9 @@ __device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4
 // m0 + 64 wm + [0, 64) and columns n0 + (BN / 2) wn + [0, BN / 2), accumulator
 // acc[i][j] the 16 x 16 block (i, j) of it.  `lds` is free when it is called
 // (STAGED: wave-private staging areas of 16 x (BN / 2 + 4) floats).
-template <int BN, bool STAGED>
-__device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)[4][BN / 32], float *lds, int m0,
+// MI: 16-row sub-tiles per wave (the tile has 64 MI rows, waves 4 x 2).
+template <int BN, bool STAGED, int MI = 4>
+__device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)[MI][BN / 32], float *lds, int m0,
                                              int n0, int wave, int lane) {
     constexpr int WN = BN / 2, NT = WN / 16;
     const int wm = wave >> 1, wn = wave & 1;
@@ -377,13 +378,13 @@ __device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)
         // The K loop ended with a barrier: LDS is free.  Wave-private staging areas.
         constexpr int SW = WN + 4;
         float *stage = lds + wave * 16 * SW;
-        const int row0 = m0 + wm * 64;
+        const int row0 = m0 + wm * 16 * MI;
         if (p.silu_pair) {
             if constexpr (BN % 128 == 0) {
                 constexpr int HW = WN / 2;  // output columns of the wave
                 const int hcol0 = (n0 + wn * WN) / 2;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (int i = 0; i < MI; ++i) {
 #pragma unroll
                     for (int b = 0; b < WN / 64; ++b)
 #pragma unroll
@@ -414,7 +415,7 @@ __device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)
         auto rows = [&](auto act_c) {
             constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < MI; ++i) {
 #pragma unroll
                 for (int j = 0; j < NT; ++j)
 #pragma unroll
@@ -459,10 +460,10 @@ __device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)
                     const int hcol = (n0 + wn * WN + 64 * b) / 2 + 16 * h + li;
                     if (hcol >= p.N / 2) continue;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
+                    for (int i = 0; i < MI; ++i)
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
+                            const int row = m0 + wm * 16 * MI + i * 16 + 4 * g4 + r;
                             if (row < p.M) {
                                 const float x = acc[i][4 * b + h][r], gt = acc[i][4 * b + 2 + h][r];
                                 p.C[(size_t)row * p.ldc + hcol] = x / (1.0f + expf(-x)) * gt;
@@ -478,10 +479,10 @@ __device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)
         if (col >= p.N) continue;
         const float bias = p.bias ? p.bias[col] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < MI; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int row = m0 + wm * 64 + i * 16 + 4 * g4 + r;
+                const int row = m0 + wm * 16 * MI + i * 16 + 4 * g4 + r;
                 if (row < p.M) {
                     float x = apply_act(acc[i][j][r] + bias, p.act);
                     if (p.residual) x += p.residual[(size_t)row * p.ldr + col];
@@ -721,10 +722,11 @@ __device__ __forceinline__ void split3_x8(floatx4 x0, floatx4 x1, bf16x8 &p1, bf
 typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr uint32_t kWaitVm0 = 0x0F70;  // s_waitcnt vmcnt(0) (expcnt / lgkmcnt left free)
 
-template <int BN, bool STAGED>
+template <int BN, bool STAGED, int MI = 4>
 __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int per_xcd) {
     constexpr int WN = BN / 2, NT = WN / 16;
-    constexpr int AB = kBigBM / 8;       // fp32 A blocks per k tile (8 rows x 32 k = 1 KB)
+    constexpr int BM = 64 * MI;          // MI 16-row sub-tiles per wave, waves 4 x 2
+    constexpr int AB = BM / 8;           // fp32 A blocks per k tile (8 rows x 32 k = 1 KB)
     constexpr int WB = BN / 16 * 3;      // W plane blocks per k tile
     constexpr int NB = AB + WB;          // 1-KB blocks per buffer
     constexpr int PER = (NB + 7) / 8;    // direct loads per wave and k tile
@@ -741,7 +743,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int 
     const int grp = flat / (GM * tiles_n), rem = flat - grp * GM * tiles_n;
     const int gm = min(GM, tiles_m - grp * GM);
     const int bm = grp * GM + rem % gm, bn = rem / gm;
-    const int m0 = bm * kBigBM, n0 = bn * BN;
+    const int m0 = bm * BM, n0 = bn * BN;
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the LDS destination goes in M0
@@ -752,7 +754,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int 
     // scalar-memory wait) before every k tile's loads.
     const int lda = __builtin_amdgcn_readfirstlane(p.lda), K = __builtin_amdgcn_readfirstlane(p.K);
     const int KT = K / 32;
-    const int rows_a = min(kBigBM, p.M - m0);
+    const int rows_a = min(BM, p.M - m0);
     const auto ra = make_rsrc(p.A + (size_t)m0 * lda, (uint32_t)(((size_t)(rows_a - 1) * lda + K) * 4));
     const auto rw = make_rsrc(p.Wp, (uint32_t)((size_t)(p.N / 16) * KT * 3 * 1024));
     const int ar = lane >> 3, apos = lane & 7;  // lane's row / LDS chunk inside an 8-row A block
@@ -775,15 +777,15 @@ __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int 
         }
     };
 
-    floatx4 acc[4][NT];
+    floatx4 acc[MI][NT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NT; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // Fragment offsets: A rows wm 64 + 16 i + li (float index), W rows wn WN + 16 j + li (bf16 index).
+    // Fragment offsets: A rows wm 16 MI + 16 i + li (float index), W rows wn WN + 16 j + li (bf16 index).
     const int fa = (li & 7) ^ (li >> 3);
-    const int offa0 = (wm * 8 + (li >> 3)) * 256 + (li & 7) * 32 + (((2 * g4) ^ fa) * 4);
-    const int offa1 = (wm * 8 + (li >> 3)) * 256 + (li & 7) * 32 + (((2 * g4 + 1) ^ fa) * 4);
+    const int offa0 = (wm * 2 * MI + (li >> 3)) * 256 + (li & 7) * 32 + (((2 * g4) ^ fa) * 4);
+    const int offa1 = (wm * 2 * MI + (li >> 3)) * 256 + (li & 7) * 32 + (((2 * g4 + 1) ^ fa) * 4);
     const int offw = (AB + wn * NT * 3) * 512 + li * 32 + ((g4 ^ x3p_swz(li)) * 8);
 
     issue(0, 0);
@@ -794,9 +796,9 @@ __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int 
         if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
         const float *base = lds + cur * NB * 256;
         const __bf16 *bh = reinterpret_cast<const __bf16 *>(base);
-        bf16x8 a1[4], a2[4], a3[4];
+        bf16x8 a1[MI], a2[MI], a3[MI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < MI; ++i) {
             const floatx4 x0 = *reinterpret_cast<const floatx4 *>(base + offa0 + i * 512);
             const floatx4 x1 = *reinterpret_cast<const floatx4 *>(base + offa1 + i * 512);
             split3_x8(x0, x1, a1[i], a2[i], a3[i]);
@@ -814,7 +816,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int 
                 nw3 = *reinterpret_cast<const bf16x8 *>(bp + 1024);
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < MI; ++i) {
                 floatx4 c = acc[i][j];
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3[i], w1, c, 0, 0, 0);
                 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[i], w3, c, 0, 0, 0);
@@ -829,7 +831,7 @@ __global__ void __launch_bounds__(kBigThreads) gemm_x3p_kernel(GemmGroup g, int 
         __builtin_amdgcn_s_waitcnt(kWaitVm0);
         lds_barrier();
     }
-    big_epilogue<BN, STAGED>(p, acc, lds, m0, n0, wave, lane);
+    big_epilogue<BN, STAGED, MI>(p, acc, lds, m0, n0, wave, lane);
 }
 
 // fp32 W [N][ldw] -> X3 planes (layout above): one thread per 8 consecutive k of a row.
@@ -1634,12 +1636,12 @@ void launch_big(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStre
         hipLaunchKernelGGL((gemm_big_kernel<BN, false, WB, X3>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
 }
 
-template <int BN>
+template <int BN, int MI = 4>
 void launch_x3p(const GemmGroup &g, int per_xcd, bool staged, dim3 grid, hipStream_t stream) {
     if (staged)
-        hipLaunchKernelGGL((gemm_x3p_kernel<BN, true>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+        hipLaunchKernelGGL((gemm_x3p_kernel<BN, true, MI>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
     else
-        hipLaunchKernelGGL((gemm_x3p_kernel<BN, false>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
+        hipLaunchKernelGGL((gemm_x3p_kernel<BN, false, MI>), grid, dim3(kBigThreads), 0, stream, g, per_xcd);
 }
 
 // The X3 form from pre-split weight planes when every product of the group
@@ -1982,6 +1984,29 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
         }
         const dim3 grid(per_xcd * kXcds, n), block(kBigThreads);
         if (use_x3(g, n) && use_x3p(g, n)) {
+            // Memory-bound shapes -- products of at most 64 columns (A read once
+            // per 64 outputs) or K <= 128 (the output write dominates) -- take
+            // 64-row tiles: four times the workgroups, each with a quarter of
+            // the A staging, so several share a CU and more loads and stores are
+            // in flight.  Same per-element product order: bit-identical.
+            int kmax = 0;
+            for (int i = 0; i < n; ++i) kmax = std::max(kmax, g.p[i].K);
+            if (bn == 64 || kmax <= 128) {
+                int small_max = 0;
+                for (int i = 0; i < n; ++i) {
+                    g.total[i] = ((g.p[i].M + 63) / 64) * g.tiles_n[i];
+                    small_max = std::max(small_max, g.total[i]);
+                }
+                const int px = (small_max + kXcds - 1) / kXcds;
+                const dim3 sgrid(px * kXcds, n);
+                switch (bn) {
+                    case 256: launch_x3p<256, 1>(g, px, staged, sgrid, stream); break;
+                    case 160: launch_x3p<160, 1>(g, px, staged, sgrid, stream); break;
+                    case 128: launch_x3p<128, 1>(g, px, staged, sgrid, stream); break;
+                    default: launch_x3p<64, 1>(g, px, staged, sgrid, stream); break;
+                }
+                return hipGetLastError();
+            }
             switch (bn) {
                 case 256: launch_x3p<256>(g, per_xcd, staged, grid, stream); break;
                 case 160: launch_x3p<160>(g, per_xcd, staged, grid, stream); break;
