@@ -132,8 +132,9 @@ def wkv_step_in_model_bytes(cfg, n: int) -> int:
 def wkv_step_in_model(engine, cfg, iters: int = 50) -> dict:
     """The decode step's own WKV-7 kernel (wkv7_step_kernel<N,true,4,true>,
     low-rank stage folded in, the first layer of the last step's stream
-    group), relaunched alone with its inputs and timed with HIP events on the
-    engine's stream (yuf_engine_time_wkv_step)."""
+    group), relaunched alone with its inputs from a replayed HIP graph and
+    timed with HIP events on the engine's stream (yuf_engine_time_wkv_step);
+    the time per launch includes the graph's dispatch gap between kernels."""
     us, n = engine.time_wkv_step(iters)
     nbytes = wkv_step_in_model_bytes(cfg, n)
     achieved = nbytes / (us * 1e-6) / 1e9

@@ -306,12 +306,14 @@ int yuf_engine_take_error(yuf_engine *eng);
  * Measurement hook (no reference counterpart): times the decode step's
  * first-layer WKV-7 step kernel -- the fused form with the second low-rank
  * stage, as the last decode step launched it (same inputs, streams and
- * launch shape) -- `iters` times on the engine's stream between HIP events,
- * writing the new state to a scratch buffer so the engine's state does not
- * change.  *avg_us receives the mean duration, *streams (if not NULL) the
- * number of streams of that launch.  Needs a prior decode step with fp32
- * weights and the fused low-rank step (else YUF_ERR_INVALID); allocates and
- * frees its scratch.
+ * launch shape) -- `iters` times, captured as one HIP graph and replayed on
+ * the engine's stream between HIP events (the decode step is graph-replayed
+ * too), writing the new state to a scratch buffer so the engine's state does
+ * not change.  *avg_us receives the mean time per launch, the graph's
+ * dispatch gap between kernels included; *streams (if not NULL) the number
+ * of streams of that launch.  Needs a prior decode step with fp32 weights
+ * and the fused low-rank step (else YUF_ERR_INVALID); allocates and frees
+ * its scratch.
  */
 int yuf_engine_time_wkv_step(yuf_engine *eng, int iters, float *avg_us, int *streams);
 

@@ -1328,16 +1328,32 @@ extern "C" int yuf_engine_time_wkv_step(yuf_engine *eng, int iters, float *avg_u
     DeviceBuf scratch;
     ENG_TRY(hipMalloc(&scratch.p, floats * sizeof(float)), "time_wkv_step scratch");
     wp.state_out = static_cast<float *>(scratch.p);
+    // The launches are captured into one HIP graph and replayed, as the
+    // decode step replays its own: back-to-back launches from the host leave
+    // a dispatch gap of ~5 us after each ~8 us kernel, which events would
+    // count as kernel time; graph-replayed kernels are ~2 us apart.
     hipEvent_t t0 = nullptr, t1 = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
     ENG_TRY(hipEventCreate(&t0), "event");
     hipError_t err = hipEventCreate(&t1);
     if (err == hipSuccess) err = launch_wkv7(wp, e.s.head_size, true, e.stream);  // warm-up
+    if (err == hipSuccess) err = hipStreamBeginCapture(e.stream, hipStreamCaptureModeThreadLocal);
+    if (err == hipSuccess) {
+        for (int i = 0; i < iters && err == hipSuccess; ++i) err = launch_wkv7(wp, e.s.head_size, true, e.stream);
+        const hipError_t end = hipStreamEndCapture(e.stream, &graph);  // always ends the capture
+        if (err == hipSuccess) err = end;
+    }
+    if (err == hipSuccess) err = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    if (err == hipSuccess) err = hipGraphLaunch(exec, e.stream);  // warm-up replay
     if (err == hipSuccess) err = hipEventRecord(t0, e.stream);
-    for (int i = 0; i < iters && err == hipSuccess; ++i) err = launch_wkv7(wp, e.s.head_size, true, e.stream);
+    if (err == hipSuccess) err = hipGraphLaunch(exec, e.stream);
     if (err == hipSuccess) err = hipEventRecord(t1, e.stream);
     if (err == hipSuccess) err = hipEventSynchronize(t1);
     float ms = 0.f;
     if (err == hipSuccess) err = hipEventElapsedTime(&ms, t0, t1);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
     hipEventDestroy(t0);
     if (t1) hipEventDestroy(t1);
     if (err != hipSuccess) return fail(YUF_ERR_HIP, std::string("time_wkv_step: ") + hipGetErrorString(err));
