@@ -248,7 +248,7 @@ def bench_gemm(iters: int) -> dict:
     peak = BF16_MFMA_PEAK_TFLOPS / 6.0
     return {"bound": "mfma", "achieved": round(tflops, 2), "peak": round(peak, 1), "unit": "TFLOP/s",
             "frac": round(tflops / peak, 4), "fp32_mfma_peak": FP32_MFMA_PEAK_TFLOPS,
-            "kernel": "gemm_x3p_kernel<256,true> (fp32 via 6 bf16 MFMAs, pre-split W planes), M=16384 N=5120 K=640",
+            "kernel": "gemm_x3p_kernel<256,true,4> (fp32 via 6 bf16 MFMAs, pre-split W planes, 256-row tiles), M=16384 N=5120 K=640",
             "avg_us": round(ms * 1e3, 1)}
 
 
