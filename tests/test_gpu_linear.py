@@ -130,8 +130,8 @@ def test_large_tile_products_hold_fp32_accuracy(m, n, k):
     (1000, 640, 2560, "residual"), (2048, 640, 640, "bias_sigmoid"),                      # 160-wide tiles
     (700, 384, 640, "alias"), (512, 128, 64, "none"),                                     # 128-wide tiles
     (300, 192, 640, "bias"), (257, 64, 32, "none"),                                       # 64-wide tiles
-    (1000, 640, 64, "bias"), (700, 640, 128, "residual"), (512, 512, 96, "bias_tanh"),    # 64-row tiles (K <= 128)
-    (300, 256, 128, "alias"),
+    (1000, 640, 64, "bias"), (700, 640, 128, "residual"),                                 # 64-row tiles (K <= 128)
+    (512, 512, 96, "bias_tanh"), (300, 256, 128, "alias"),       # K <= 128 at 256 wide: 256-row tiles
     (1000, 48, 64, "none"),   # no large-tile width fits: the planes are not used
     (64, 640, 640, "none"),   # decode path: the planes are not used
     (999, 640, 640, "offset"),   # A rows not 16-byte aligned: W is split by the kernel as before

@@ -1986,12 +1986,15 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
         if (use_x3(g, n) && use_x3p(g, n)) {
             // Memory-bound shapes -- products of at most 64 columns (A read once
             // per 64 outputs) or K <= 128 (the output write dominates) -- take
-            // 64-row tiles: four times the workgroups, each with a quarter of
-            // the A staging, so several share a CU and more loads and stores are
-            // in flight.  Same per-element product order: bit-identical.
+            // 64-row tiles when the tile is at most 160 wide: four times the
+            // workgroups, each with at most 76 KB of LDS, so two or more share
+            // a CU and more loads and stores are in flight.  (64 x 256 tiles
+            // hold 112 KB, one per CU, and 64 x 128 tiles in place of 256 x
+            // 256 ones were measured slower.)  Same per-element product order:
+            // bit-identical.
             int kmax = 0;
             for (int i = 0; i < n; ++i) kmax = std::max(kmax, g.p[i].K);
-            if (bn == 64 || kmax <= 128) {
+            if (bn == 64 || (kmax <= 128 && bn <= 160)) {
                 int small_max = 0;
                 for (int i = 0; i < n; ++i) {
                     g.total[i] = ((g.p[i].M + 63) / 64) * g.tiles_n[i];
@@ -2000,7 +2003,6 @@ hipError_t launch_gemm_group(const GemmParams *ps, int count, hipStream_t stream
                 const int px = (small_max + kXcds - 1) / kXcds;
                 const dim3 sgrid(px * kXcds, n);
                 switch (bn) {
-                    case 256: launch_x3p<256, 1>(g, px, staged, sgrid, stream); break;
                     case 160: launch_x3p<160, 1>(g, px, staged, sgrid, stream); break;
                     case 128: launch_x3p<128, 1>(g, px, staged, sgrid, stream); break;
                     default: launch_x3p<64, 1>(g, px, staged, sgrid, stream); break;
