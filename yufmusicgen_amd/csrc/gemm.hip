@@ -357,11 +357,11 @@ __device__ __forceinline__ float4 stage_read(const float *stage, int row, int c4
     return *reinterpret_cast<const float4 *>(stage + row * (WN + 4) + 4 * c4);
 }
 
-// Epilogue of the large-tile kernels: waves 4 x 2, wave (wm, wn) owns rows
-// m0 + 64 wm + [0, 64) and columns n0 + (BN / 2) wn + [0, BN / 2), accumulator
-// acc[i][j] the 16 x 16 block (i, j) of it.  `lds` is free when it is called
+// Epilogue of the large-tile kernels: waves 4 x 2 over a 64 MI x BN tile, wave
+// (wm, wn) owns rows m0 + 16 MI wm + [0, 16 MI) and columns n0 + (BN / 2) wn +
+// [0, BN / 2), accumulator acc[i][j] the 16 x 16 block (i, j) of it (MI = 4:
+// 256-row tiles; MI = 1: 64-row tiles).  `lds` is free when it is called
 // (STAGED: wave-private staging areas of 16 x (BN / 2 + 4) floats).
-// MI: 16-row sub-tiles per wave (the tile has 64 MI rows, waves 4 x 2).
 template <int BN, bool STAGED, int MI = 4>
 __device__ __forceinline__ void big_epilogue(const GemmParams &p, floatx4 (&acc)[MI][BN / 32], float *lds, int m0,
                                              int n0, int wave, int lane) {
@@ -698,11 +698,12 @@ __global__ void __launch_bounds__(kBigThreads) gemm_big_kernel(GemmGroup g, int 
 // two buffers while the MFMAs run on the other -- A as fp32 in 8-row x 32-k
 // blocks (chunk c of row R at c ^ (R & 7) ^ ((R >> 3) & 1), conflict-free for
 // the fragment reads), W as its plane blocks -- with one barrier per k tile.
-// Each wave splits its own 64 A rows into parts (two waves share rows: the
-// split is done twice), W's parts come ready from LDS.  Tile 256 x BN, waves
-// 4 x 2 as in gemm_big_kernel; the per-32-k product order and the split are
-// the X3 form's, so the results are bit-identical to it.  LDS: two buffers of
-// 32 KB (A) + 6 BN / 16 KB (W planes): 160 KB at BN = 256.
+// Each wave splits its own 16 MI A rows into parts (two waves share rows: the
+// split is done twice), W's parts come ready from LDS.  Tile 64 MI x BN,
+// waves 4 x 2 as in gemm_big_kernel (MI = 4: 256 rows; MI = 1: 64 rows for the
+// memory-bound shapes); the per-32-k product order and the split are the X3
+// form's, so the results are bit-identical to it.  LDS: two buffers of 8 MI
+// KB (A) + 6 BN / 16 KB (W planes): 160 KB at BN = 256, MI = 4.
 __host__ __device__ constexpr int x3p_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
 __device__ __forceinline__ void split3_x8(floatx4 x0, floatx4 x1, bf16x8 &p1, bf16x8 &p2, bf16x8 &p3) {
